@@ -1,0 +1,248 @@
+"""Benchmark of the NF4-LoRA projection path on one MI355X.
+
+Workload ("C3"): one MQA decoder layer's seven NF4-LoRA
+projections, forward + backward, at 8192 packed tokens, d_model 4096, one KV head
+(k/v out 128), SwiGLU intermediate 11008, LoRA rank 256 (fp32 adapters, unit scaling), NF4
+bases quantized from ~N(0, 0.02). One step = the reference's operator calls for the layer:
+project_group((q, k, v), x), project_group((o,), y), project_group((gate, up), x2),
+project_group((down,), h), then autograd backward with ~N(0, 1) upstream gradients
+(input gradients and fp32 dA/dB for all seven). Synthetic data, random-init weights.
+
+value  = algorithmic TFLOP/s of the step, 2M[2KN + 3r(K+N)] summed over the seven
+         projections (6.449 TFLOP; the reference's xa recompute is not counted).
+Also reported on the same line: the dominant kernel's roofline (HIP-event timed), the
+standalone NF4 dequant of C2 (GB/s vs 8 TB/s), a hipBLASLt bf16 GEMM probe, and the
+reference op sequence timed on the host CPU (cpu_baseline).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "causal-tuner_amd"))
+
+import torch  # noqa: E402
+
+METRIC = "NF4-LoRA proj fwd+bwd TFLOP/s; NF4 dequant GB/s; train tokens/sec (1 GPU)"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+T, D, KV, I, R = 8192, 4096, 128, 11008, 256
+SPECS = [("q", D, D, True), ("k", D, KV, True), ("v", D, KV, True), ("o", D, D, False),
+         ("gate", D, I, False), ("up", D, I, False), ("down", I, D, False)]
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def projection_flops(m, k, n, r):
+    return 2 * m * (2 * k * n + 3 * r * (k + n))
+
+
+def step_flops(tokens=T):
+    return sum(projection_flops(tokens, k, n, R) for _, k, n, _ in SPECS)
+
+
+def build_layer(device, tokens=T, seed=0):
+    from causal_tuner.modeling.lora import Projection
+    torch.manual_seed(seed)
+    modules = {}
+    for name, k, n, bias in SPECS:
+        module = Projection(k, n, bias=bias, rank=R, device=device)
+        if device != "cpu":
+            module.install_nf4(module.weight.detach().clone(), device)
+        torch.nn.init.normal_(module.lora_B, std=0.01)
+        modules[name] = module
+    g = torch.Generator(device=device).manual_seed(seed + 1)
+    inputs = {key: torch.randn(tokens, width, device=device, generator=g).to(torch.bfloat16).requires_grad_(True)
+              for key, width in (("x", D), ("y", D), ("x2", D), ("h", I))}
+    grads = {name: torch.randn(tokens, n, device=device, generator=g).to(torch.bfloat16)
+             for name, _, n, _ in SPECS}
+    return modules, inputs, grads
+
+
+def layer_step(modules, inputs, grads):
+    from causal_tuner.kernels.linear import project_group
+    m = modules
+    q, k, v = project_group((m["q"], m["k"], m["v"]), inputs["x"])
+    o, = project_group((m["o"],), inputs["y"])
+    gate, up = project_group((m["gate"], m["up"]), inputs["x2"])
+    down, = project_group((m["down"],), inputs["h"])
+    outputs = (q, k, v, o, gate, up, down)
+    wrt = [inputs[key] for key in ("x", "y", "x2", "h")]
+    for name in ("q", "k", "v", "o", "gate", "up", "down"):
+        wrt += [m[name].lora_A, m[name].lora_B]
+    return torch.autograd.grad(outputs, wrt, [grads[n] for n in ("q", "k", "v", "o", "gate", "up", "down")])
+
+
+def time_events(fn, iters, warmup=3):
+    """Average duration (ms) of fn() on the current stream, bracketed by HIP events."""
+    for _ in range(warmup):
+        fn()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        fn()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / iters
+
+
+def dominant_kernel_roofline(device):
+    """The base NT GEMM of the largest projection (gate: 8192 x 4096 -> 11008), the
+    instantiation that carries most of the step's MFMA work, timed alone with HIP events."""
+    from causal_tuner.kernels import _native
+    lib = _native.library()
+    x = torch.randn(T, D, device=device).to(torch.bfloat16)
+    w = (torch.randn(I, D, device=device) * 0.02).to(torch.bfloat16)
+    out = torch.empty(T, I, device=device, dtype=torch.bfloat16)
+    stream = _native.stream_of(x)
+
+    def run():
+        status = lib.ct_gemm(x.data_ptr(), D, 0, w.data_ptr(), D, 1, out.data_ptr(), I, _native.CT_BF16, None, 0,
+                             T, I, D, stream)
+        assert status == 0
+    ms = time_events(run, 20)
+    flops = 2.0 * T * I * D
+    achieved = flops / (ms * 1e-3) / 1e12
+    ms_torch = time_events(lambda: torch.mm(x, w.T, out=out), 20)
+    return {"kernel": "gemm_kernel<128,128,2,KC,KC,vec,bf16> (ct_gemm NT: 8192x4096 . 4096x11008)",
+            "bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None, "avg_ms": round(ms, 4),
+            "flops_per_launch": flops,
+            "hipblaslt_probe_tflops": round(flops / (ms_torch * 1e-3) / 1e12, 2)}
+
+
+def dequant_measure(device):
+    """C2: standalone NF4 dequant of [28672, 8192] (and [8192, 8192]) to bf16, HBM GB/s."""
+    from causal_tuner.kernels.nf4_cuda import dequantize_nf4_into
+    from causal_tuner.quant.nf4 import quantize_nf4
+    results = {}
+    for rows, cols, copies in ((28672, 8192, 1), (8192, 8192, 3)):
+        n = rows * cols
+        nb, nb2 = -(-n // 64), -(-n // (64 * 256))
+        moved = n / 2 + nb + 4 * nb2 + 64 + 1024 + 4 + 2 * n
+        weights = []
+        for c in range(copies):  # rotate copies so the 256 MB Infinity Cache cannot hold the working set
+            w = (torch.randn(rows, cols, device=device) * 0.02).to(torch.bfloat16)
+            packed, state = quantize_nf4(w)
+            del w
+            weights.append((packed, state, torch.empty(rows, cols, device=device, dtype=torch.bfloat16)))
+        index = [0]
+
+        def run():
+            packed, state, out = weights[index[0] % copies]
+            index[0] += 1
+            dequantize_nf4_into(packed, state, out)
+        ms = time_events(run, 30)
+        gbs = moved / (ms * 1e-3) / 1e9
+        results[f"{rows}x{cols}"] = {"GB/s": round(gbs, 1), "avg_us": round(ms * 1e3, 2), "bytes": int(moved),
+                                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del weights
+    return results
+
+
+def cpu_baseline(budget_s=12.0):
+    """The reference's torch-op sequence (oracle/lora.py) on the host CPU, bf16, for the
+    seven C3 projections over a bounded token sample."""
+    from oracle import lora as olora
+    tokens = 1024
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(3)
+    layers = []
+    for name, k, n, bias in SPECS:
+        w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16)
+        a = (torch.rand(R, k, generator=g) * 2 - 1) * (6 / k) ** 0.5
+        b = torch.randn(n, R, generator=g) * 0.01
+        x = torch.randn(tokens, k, generator=g).to(torch.bfloat16)
+        dy = torch.randn(tokens, n, generator=g).to(torch.bfloat16)
+        layers.append((w, a, b, x, dy, torch.zeros(n, dtype=torch.bfloat16) if bias else None))
+
+    def run():
+        for w, a, b, x, dy, bias in layers:
+            olora.reference_forward(x, w, a, b, bias)
+            olora.reference_backward(x, w, a, b, dy)
+    run()
+    reps, start = 0, time.perf_counter()
+    while True:
+        run()
+        reps += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= budget_s or reps >= 50:
+            break
+    flops = step_flops(tokens) * reps
+    return {"value": round(flops / elapsed / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"reference torch-op sequence (oracle/lora.py), bf16 on CPU, seven C3 projections "
+                      f"fwd+bwd at {tokens} of {T} tokens, {reps} reps in {elapsed:.1f} s"}
+
+
+def main():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=10)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs the MI355X (no HIP device visible)", file=sys.stderr)
+        sys.exit(2)
+    device = "cuda"
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    log("building C3 layer (NF4 quantization of seven projections)...")
+    modules, inputs, grads = build_layer(device)
+    for _ in range(args.warmup):
+        layer_step(modules, inputs, grads)
+    torch.cuda.synchronize()
+    log(f"warmup done; timing {args.steps} steps")
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        layer_step(modules, inputs, grads)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    ms_per_step = elapsed * 1e3 / args.steps
+    tflops = step_flops() / (ms_per_step * 1e-3) / 1e12
+    log(f"C3 step: {ms_per_step:.3f} ms, {tflops:.1f} TFLOP/s")
+    del modules, inputs, grads
+    torch.cuda.empty_cache()
+
+    roofline = dominant_kernel_roofline(device)
+    log(f"dominant kernel: {roofline}")
+    dequant = dequant_measure(device)
+    log(f"dequant: {dequant}")
+    cpu = None if args.no_cpu else cpu_baseline()
+    log(f"cpu baseline: {cpu}")
+
+    line = {
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: X, upstream grads ~N(0,1) bf16; NF4 bases from ~N(0,0.02); LoRA A Kaiming-uniform, "
+                "B ~N(0,0.01), fp32, rank 256, random init",
+        "config": {"workload": "C3: one MQA decoder layer's seven NF4-LoRA projections fwd+bwd "
+                               "(q,k,v,o,gate,up,down), 8192 tokens, d 4096, kv 128, I 11008, r 256",
+                   "tokens": T, "d_model": D, "kv_out": KV, "intermediate": I, "rank": R,
+                   "flops_per_step": step_flops()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "dequant": {"workload": "C2: standalone NF4 dequant to bf16", "bound": "hbm", "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "results": dequant},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,113 @@
+"""ctypes binding of the C ABI in include/causal_tuner_hip.h (lib/libcausal_tuner_hip.so).
+
+torch is imported first so that the library's libamdhip64.so.7 dependency resolves to the
+HIP runtime torch already mapped; the streams and device pointers passed across the
+boundary therefore belong to the same runtime. A missing library raises RuntimeError:
+there is no fallback.
+"""
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+DEFAULT_LIBRARY = os.path.normpath(os.path.join(_HERE, "..", "..", "lib", "libcausal_tuner_hip.so"))
+
+CT_F32, CT_F16, CT_BF16 = 0, 1, 2
+DTYPE_CODES = {torch.float32: CT_F32, torch.float16: CT_F16, torch.bfloat16: CT_BF16}
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+
+
+class NF4Weight(ctypes.Structure):
+    """Mirror of `ct_nf4_weight`: the QuantState fields the decoder reads."""
+
+    _fields_ = [
+        ("packed", _P), ("absmax", _P), ("code", _P), ("code2", _P), ("absmax2", _P), ("offset", _P),
+        ("rows", _I64), ("cols", _I64), ("blocksize", _I32), ("blocksize2", _I32), ("nested", _I32),
+        ("storage_dtype", _I32),
+    ]
+
+
+_SIGNATURES = {
+    "ct_abi_version": (ctypes.c_int, []),
+    "ct_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "ct_nf4_dequant": (ctypes.c_int, [ctypes.POINTER(NF4Weight), _P, _I32, _P]),
+    "ct_gemm": (ctypes.c_int, [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _P, _I32, _I64, _I64, _I64, _P]),
+    "ct_forward_linear": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _P, _I64, _P,
+                                         _I64, _I64, _I64, _I64, _P]),
+    "ct_input_gradient": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _I64, _P,
+                                         _I64, _I64, _I64, _I64, _I32, _P]),
+    "ct_parameter_gradients_workspace": (_I64, [_I64, _I64, _I64, _I64]),
+    "ct_parameter_gradients": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32,
+                                              _P, _I64, _P]),
+    "ct_accumulate_workspace": (_I64, [_I64, _I64, _I64]),
+    "ct_accumulate": (ctypes.c_int, [_P, _I64, _P, _I64, _I32, _P, _I64, _I32, _I64, _I64, _I64, _I32, _P, _I64,
+                                     _P]),
+}
+
+# Every symbol the header declares; tests check the built library exports each one.
+EXPORTED = tuple(_SIGNATURES)
+
+_library = None
+
+
+def library_path():
+    return os.environ.get("CAUSAL_TUNER_HIP_LIBRARY", DEFAULT_LIBRARY)
+
+
+def library():
+    """Load (once) and return the HIP library with its C signatures declared."""
+    global _library
+    if _library is None:
+        path = library_path()
+        if not os.path.exists(path):
+            raise RuntimeError(f"The HIP library {path} is not built; run `python causal-tuner_amd/build.py`")
+        lib = ctypes.CDLL(path)
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = restype, argtypes
+        _library = lib
+    return _library
+
+
+def check(status, what):
+    if status != 0:
+        message = library().ct_status_string(status).decode()
+        raise RuntimeError(f"{what} failed with status {status}: {message}")
+
+
+def stream_of(tensor):
+    """The caller's current HIP stream on the tensor's device (kernels never pick their own)."""
+    return ctypes.c_void_p(torch.cuda.current_stream(tensor.device).cuda_stream)
+
+
+def ptr(tensor):
+    return None if tensor is None else ctypes.c_void_p(tensor.data_ptr())
+
+
+def dtype_code(dtype):
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise ValueError(f"Unsupported element type {dtype}") from None
+
+
+def nf4_descriptor(weight, state):
+    """Build the ct_nf4_weight view of a packed weight and its QuantState (no copies)."""
+    nested = bool(state.nested)
+    aux = state.state2 if nested else None
+    numel = 1
+    for size in state.shape:
+        numel *= int(size)
+    rows = int(state.shape[0]) if len(state.shape) >= 2 else 1
+    cols = numel // rows if rows else 0
+    desc = NF4Weight(
+        packed=weight.data_ptr(), absmax=state.absmax.data_ptr(), code=state.code.data_ptr(),
+        code2=aux.code.data_ptr() if nested else None, absmax2=aux.absmax.data_ptr() if nested else None,
+        offset=state.offset.data_ptr() if nested else None, rows=rows, cols=cols, blocksize=int(state.blocksize),
+        blocksize2=int(aux.blocksize) if nested else 0, nested=int(nested), storage_dtype=dtype_code(state.dtype))
+    return desc

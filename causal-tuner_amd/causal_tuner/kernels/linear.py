@@ -1,0 +1,337 @@
+"""Shared-input LoRA projections with bounded workspaces and FP32 adapter gradients, on gfx950.
+
+Same operator API as the reference's kernels/linear.py (`materialize` 6-13, `accumulate`
+16-24, `forward_linear` 27-33, `input_gradient` 36-39, `parameter_gradients` 42-44,
+`projection_parameters` 47-50, `can_fuse` 53-56, `_LoRAGroup` 59-130, `project_group`
+133-148). On the device, every contraction runs in the HIP GEMMs of
+lib/libcausal_tuner_hip.so:
+
+* forward_linear: `ct_forward_linear`, xa = x a^T then out = [x | xa] [w | b]^T (+ bias):
+  the base GEMM and the rank-r epilogue are one MFMA contraction over k + r columns,
+  rounded to bf16 once;
+* input_gradient: `ct_input_gradient`, low = dy b then dx = [dy | low] [w ; a] (+ dx);
+* parameter_gradients / accumulate: `ct_parameter_gradients` / `ct_accumulate`, fp32
+  outputs with a fixed-order split reduction over tokens (repeated backward is
+  bit-identical; add=False ignores the destination's contents).
+
+The bf16 path is the device path. CPU tensors keep the reference's torch semantics (its
+unfused CPU route); device tensors of another compute dtype raise NotImplementedError.
+"""
+
+import torch
+
+from . import _native
+
+
+# ----------------------------------------------------------------------------- helpers
+def _device_bf16(*tensors):
+    return all(t.is_cuda and t.dtype == torch.bfloat16 for t in tensors if t is not None)
+
+
+def _unsupported(what, *tensors):
+    dtypes = sorted({str(t.dtype) for t in tensors if t is not None})
+    raise NotImplementedError(f"{what}: the HIP path computes in bfloat16 on the device (got {', '.join(dtypes)})")
+
+
+def _rows(t):
+    """(tensor, leading dimension) of a matrix with unit stride along its rows."""
+    if t.dim() != 2:
+        raise ValueError("expected a matrix")
+    if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+        if t.shape[0] <= 1 and t.stride(1) == 1:
+            return t, max(t.shape[1], 1)
+        t = t.contiguous()
+    return t, t.stride(0)
+
+
+def _operand(t):
+    """(tensor, ld, transposed) for a bf16 matrix given as a row- or column-major view."""
+    if t.stride(1) == 1 and t.stride(0) >= t.shape[1]:
+        return t, t.stride(0), 0
+    if t.stride(0) == 1 and t.stride(1) >= t.shape[0]:
+        return t, t.stride(1), 1
+    t = t.contiguous()
+    return t, max(t.shape[1], 1), 0
+
+
+def _workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+class _Output:
+    """A caller's output view; kernels write a contiguous stand-in when the view is strided."""
+
+    def __init__(self, target):
+        self.target = target
+        ok = target.dim() == 2 and target.stride(1) == 1 and target.stride(0) >= target.shape[1]
+        self.buffer = target if ok else torch.empty(target.shape, dtype=target.dtype, device=target.device)
+        self.ld = max(self.buffer.stride(0), self.buffer.shape[1], 1)
+
+    def finish(self):
+        if self.buffer is not self.target:
+            self.target.copy_(self.buffer)
+
+
+class _Contiguous(_Output):
+    def __init__(self, target):
+        self.target = target
+        self.buffer = target if target.is_contiguous() else torch.empty(target.shape, dtype=target.dtype,
+                                                                        device=target.device)
+        self.ld = max(target.shape[-1], 1)
+
+
+# ----------------------------------------------------------------------------- operators
+def materialize(weight, state, dtype):
+    if state is not None:
+        if state.quant_type != "nf4":
+            raise ValueError(f"Unsupported quantization type {state.quant_type!r}")
+        if not weight.is_cuda:
+            raise RuntimeError("NF4 weights decode on the HIP device only")
+        from .nf4_cuda import dequantize_nf4
+        return dequantize_nf4(weight.contiguous(), state, dtype)
+    return weight.to(dtype)
+
+
+def accumulate(output, left, right, *, add=True):
+    beta = 1 if add else 0
+    if output.dtype == torch.float32 and left.dtype == torch.bfloat16 and left.is_cuda:
+        if right.dtype != torch.bfloat16:
+            _unsupported("accumulate", left, right)
+        p, j = left.shape
+        q = right.shape[1]
+        target = _Output(output)
+        lt, ldl, tl = _operand(left)
+        rt, ldr, tr = _operand(right)
+        lib = _native.library()
+        ws = _workspace(lib.ct_accumulate_workspace(p, q, j), output.device)
+        with torch.cuda.device(output.device):
+            status = lib.ct_accumulate(_native.ptr(target.buffer), target.ld, _native.ptr(lt), ldl, tl,
+                                       _native.ptr(rt), ldr, tr, p, q, j, int(add) if target.buffer is output else
+                                       0, _native.ptr(ws), ws.numel(), _native.stream_of(output))
+        _native.check(status, "ct_accumulate")
+        if target.buffer is not output:
+            output.copy_(target.buffer + output if add else target.buffer)
+    elif left.is_cuda:
+        _unsupported("accumulate", output, left, right)
+    elif output.dtype != left.dtype:
+        output.addmm_(left.to(output.dtype), right.to(output.dtype), beta=beta)
+    else:
+        output.addmm_(left, right, beta=beta)
+
+
+def forward_linear(x, weight, a, b, *, out, xa, bias=None):
+    if not x.is_cuda:
+        if bias is None:
+            torch.mm(x, weight.T, out=out)
+        else:
+            torch.addmm(bias, x, weight.T, out=out)
+        torch.mm(x, a.T, out=xa)
+        out.addmm_(xa, b.T)
+        return
+    if not _device_bf16(x, weight, a, b, out, xa, bias):
+        _unsupported("forward_linear", x, weight, a, b, out, xa, bias)
+    _forward(x, weight, None, a, b, bias, out, xa)
+
+
+def _forward(x, weight, state, a, b, bias, out, xa):
+    m, k = x.shape
+    n, r = out.shape[1], a.shape[0]
+    x, ldx = _rows(x)
+    w = None if weight is None else weight.contiguous()
+    a, b = a.contiguous(), b.contiguous()
+    bias = None if bias is None else bias.contiguous()
+    target, low = _Output(out), _Contiguous(xa)
+    desc = None if state is None else _native.nf4_descriptor(w, state)
+    with torch.cuda.device(x.device):
+        status = _native.library().ct_forward_linear(
+            _native.ptr(x), ldx, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),
+            _native.ptr(b), _native.ptr(bias), _native.ptr(target.buffer), target.ld, _native.ptr(low.buffer),
+            m, n, k, r, _native.stream_of(x))
+    _native.check(status, "ct_forward_linear")
+    target.finish()
+    low.finish()
+
+
+def input_gradient(dy, weight, a, b, dx, low, *, add=False):
+    if not dy.is_cuda:
+        torch.mm(dy, b, out=low)
+        torch.addmm(dx, dy, weight, beta=1 if add else 0, out=dx)
+        dx.addmm_(low, a)
+        return
+    if not _device_bf16(dy, weight, a, b, dx, low):
+        _unsupported("input_gradient", dy, weight, a, b, dx, low)
+    _input_gradient(dy, weight, None, a, b, dx, low, add)
+
+
+def _input_gradient(dy, weight, state, a, b, dx, low, add):
+    m, n = dy.shape
+    k, r = dx.shape[1], a.shape[0]
+    dy, lddy = _rows(dy)
+    w = None if weight is None else weight.contiguous()
+    a, b = a.contiguous(), b.contiguous()
+    target, lowc = _Output(dx), _Contiguous(low)
+    if add and target.buffer is not dx:
+        target.buffer.copy_(dx)
+    desc = None if state is None else _native.nf4_descriptor(w, state)
+    with torch.cuda.device(dy.device):
+        status = _native.library().ct_input_gradient(
+            _native.ptr(dy), lddy, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),
+            _native.ptr(b), _native.ptr(target.buffer), target.ld, _native.ptr(lowc.buffer), m, n, k, r, int(add),
+            _native.stream_of(dy))
+    _native.check(status, "ct_input_gradient")
+    target.finish()
+    lowc.finish()
+
+
+def parameter_gradients(x, dy, da, db, low, xa, *, add):
+    if not x.is_cuda:
+        accumulate(da, low.T, x, add=add)
+        accumulate(db, dy.T, xa, add=add)
+        return
+    if not (_device_bf16(x, dy, low, xa) and da.dtype == db.dtype == torch.float32):
+        accumulate(da, low.T, x, add=add)
+        accumulate(db, dy.T, xa, add=add)
+        return
+    m, k = x.shape
+    n, r = dy.shape[1], low.shape[1]
+    x, ldx = _rows(x)
+    dy, lddy = _rows(dy)
+    low, xa = low.contiguous(), xa.contiguous()
+    if not (da.is_contiguous() and db.is_contiguous()):
+        accumulate(da, low.T, x, add=add)
+        accumulate(db, dy.T, xa, add=add)
+        return
+    lib = _native.library()
+    ws = _workspace(lib.ct_parameter_gradients_workspace(m, n, k, r), x.device)
+    with torch.cuda.device(x.device):
+        status = lib.ct_parameter_gradients(_native.ptr(x), ldx, _native.ptr(dy), lddy, _native.ptr(low),
+                                             _native.ptr(xa), _native.ptr(da), _native.ptr(db), m, n, k, r,
+                                             int(add), _native.ptr(ws), ws.numel(), _native.stream_of(x))
+    _native.check(status, "ct_parameter_gradients")
+
+
+def projection_parameters(module):
+    weight = module.weight if module.quantized is None else module.quantized.weight
+    state = None if module.quantized is None else weight.quant_state
+    return (weight, module.lora_A, module.lora_B, module.bias), state
+
+
+def can_fuse(module, x):
+    return (x.is_cuda and module.rank and not (module.bias is not None and module.bias.requires_grad)
+            and (module.weight is None or not module.weight.requires_grad)
+            and module.lora_A.requires_grad and module.lora_B.requires_grad)
+
+
+# ----------------------------------------------------------------------------- grouped autograd
+class _LoRAGroup(torch.autograd.Function):
+    """Projections sharing one input; saves only the input and parameters (linear.py:59-130)."""
+
+    @staticmethod
+    def forward(ctx, x, dtype, tile, states, cosine, sine, head_dim, residual, *parameters):
+        ctx.save_for_backward(x, cosine, sine, *parameters)
+        ctx.dtype, ctx.tile, ctx.states = dtype, tile or 4096, states
+        ctx.head_dim = head_dim
+        flat = x.reshape(-1, x.shape[-1]).to(dtype)
+        outputs = []
+        rows = min(ctx.tile, len(flat)) if tile else len(flat)
+        for index, state in enumerate(states):
+            weight, a, b, bias = parameters[index*4:index*4+4]
+            matrix, ac, bc = materialize(weight, state, dtype), a.to(dtype), b.to(dtype)
+            bias = None if bias is None else bias.to(dtype)
+            out = torch.empty((len(flat), len(matrix)), device=x.device, dtype=dtype)
+            low = torch.empty((rows, len(a)), device=x.device, dtype=dtype)
+            # The untiled path is one fused contraction over all rows; explicit tiles bound
+            # the rank-r workspace to `tile` rows as in the reference.
+            step = tile or max(len(flat), 1)
+            for start in range(0, len(flat), step):
+                part = flat[start:start+step]
+                forward_linear(part, matrix, ac, bc, bias=bias, out=out[start:start+step], xa=low[:len(part)])
+            outputs.append(out.reshape(*x.shape[:-1], len(matrix)))
+            del matrix, ac, bc, low
+        if head_dim:
+            from .core_cuda import rotate_owned_qk
+            rotate_owned_qk(outputs[0], outputs[1], cosine, sine, head_dim)
+        if residual is not None:
+            outputs[0].add_(residual)
+        return tuple(outputs)
+
+    @staticmethod
+    def backward(ctx, *grad_outputs):
+        x, cosine, sine, *parameters = ctx.saved_tensors
+        flat = x.reshape(-1, x.shape[-1]).to(ctx.dtype)
+        dx = torch.empty_like(flat) if ctx.needs_input_grad[0] else None
+        if ctx.head_dim:
+            cosine, sine = (value.reshape(-1, value.shape[-1]) for value in (cosine, sine))
+        rows = min(ctx.tile, len(flat))
+        rotary = (torch.empty(rows*max(len(b) for b in parameters[2:8:4]), device=x.device, dtype=ctx.dtype)
+                  if ctx.head_dim else None)
+        results = []
+        for index, (state, grad) in enumerate(zip(ctx.states, grad_outputs)):
+            weight, a, b, _ = parameters[index*4:index*4+4]
+            matrix = materialize(weight, state, ctx.dtype) if dx is not None else None
+            ac, bc = a.to(ctx.dtype), b.to(ctx.dtype)
+            dy = grad.reshape(-1, grad.shape[-1]).to(ctx.dtype)
+            allocate = torch.empty_like if len(flat) else torch.zeros_like
+            da, db = allocate(a), allocate(b)
+            low = torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype)
+            xa = torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype)
+            rotate = ctx.head_dim and index < 2
+            for start in range(0, len(flat), ctx.tile):
+                stop = start+ctx.tile
+                signal = dy[start:stop]
+                if rotate:
+                    from .core_cuda import inverse_rope_tile
+                    target = rotary[:signal.numel()].view_as(signal)
+                    signal = inverse_rope_tile(signal, cosine[start:stop], sine[start:stop], ctx.head_dim, target)
+                part_low, part_xa = low[:len(signal)], xa[:len(signal)]
+                if dx is not None:
+                    input_gradient(signal, matrix, ac, bc, dx[start:stop], part_low, add=index > 0)
+                else:
+                    _low_rank(signal, bc, part_low, transpose=False)
+                _low_rank(flat[start:stop], ac, part_xa, transpose=True)
+                parameter_gradients(flat[start:stop], signal, da, db, part_low, part_xa, add=start > 0)
+            results.extend((None, da, db, None))
+            del matrix, ac, bc, dy
+        residual_grad = grad_outputs[0] if ctx.needs_input_grad[7] else None
+        return (None if dx is None else dx.reshape_as(x).to(x.dtype), None, None, None, None, None, None,
+                residual_grad, *results)
+
+
+def _low_rank(x, factor, out, *, transpose):
+    """out = x factor^T (transpose) or x factor: the rank-r products torch.mm computes in
+    the reference (linear.py:124-125, mlp_cuda.py:134,140)."""
+    if not x.is_cuda:
+        torch.mm(x, factor.T if transpose else factor, out=out)
+        return
+    if not _device_bf16(x, factor, out):
+        _unsupported("low-rank product", x, factor, out)
+    m, k = x.shape
+    r = out.shape[1]
+    x, ldx = _rows(x)
+    factor = factor.contiguous()
+    target = _Output(out)
+    with torch.cuda.device(x.device):
+        status = _native.library().ct_gemm(_native.ptr(x), ldx, 0, _native.ptr(factor),
+                                           k if transpose else r, int(transpose), _native.ptr(target.buffer),
+                                           target.ld, _native.CT_BF16, None, 0, m, r, k, _native.stream_of(x))
+    _native.check(status, "ct_gemm")
+    target.finish()
+
+
+def project_group(modules, x, tile=0, *, rotary=None, residual=None):
+    if residual is not None:
+        if len(modules) != 1:
+            raise ValueError("Residual fusion requires one output projection")
+        shape = (*x.shape[:-1], len(modules[0].lora_B))
+        if residual.shape != shape or residual.dtype != modules[0].compute_dtype:
+            return (project_group(modules, x, tile, rotary=rotary)[0]+residual,)
+    parameters, states = [], []
+    for module in modules:
+        values, state = projection_parameters(module)
+        parameters.extend(values)
+        states.append(state)
+    cosine, sine, head_dim = (None, None, 0) if rotary is None else rotary
+    if rotary is not None:
+        cosine, sine = cosine.contiguous(), sine.contiguous()
+    return _LoRAGroup.apply(x, modules[0].compute_dtype, tile, tuple(states), cosine, sine, head_dim, residual,
+                            *parameters)

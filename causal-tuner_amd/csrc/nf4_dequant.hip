@@ -1,0 +1,208 @@
+// Standalone NF4 dequantization for gfx950: the MI355X replacement of the reference's
+// single-launch Triton decoder (kernels/nf4_cuda.py:9-43, `_decode` + `dequantize_nf4`).
+//
+// Decoding rule (kernels/nf4_cuda.py:16-29), for element e of a weight with N elements:
+//   g      = e / blocksize                                         first-level block
+//   s[g]   = code2[absmax[g]] * absmax2[g / blocksize2] + offset   nested (fp32 mul, then add)
+//          = absmax[g]                                             otherwise
+//   byte   = packed[e / 2];  nibble = e even ? byte >> 4 : byte & 15
+//   out[e] = out_dtype(storage_dtype(code[nibble] * s[g]))
+//
+// The vector kernel moves 8 elements per lane per step: a 4-byte load of packed nibbles
+// and one 16-byte store (two for fp32 output), each coalesced across the wavefront. The
+// 16-entry code book and the 256-entry second-level code book sit in LDS, so every lookup
+// is an LDS read whose 16 (resp. 256) fp32 entries occupy distinct banks.
+
+#include "common.hpp"
+
+namespace ct {
+namespace {
+
+constexpr int kDequantThreads = 256;
+constexpr int kChunksPerThread = 4;  // 8-element chunks per lane per launch slot
+
+template <int STORAGE, int OUT>
+__device__ __forceinline__ uint32_t encode_pair(float v0, float v1) {
+    // Two decoded values -> one 32-bit word of a 16-bit output type, element v0 first.
+    float r0 = round_to_storage<STORAGE>(v0);
+    float r1 = round_to_storage<STORAGE>(v1);
+    if constexpr (OUT == CT_BF16) return pack_bf16x2(r0, r1);
+    else return (uint32_t)f16_bits(r0) | ((uint32_t)f16_bits(r1) << 16);
+}
+
+// Vector path: requires N % 8 == 0 and 8 | blocksize (every bitsandbytes block size).
+template <bool NESTED, int STORAGE, int OUT>
+__global__ __launch_bounds__(kDequantThreads) void nf4_dequant_vec(
+    const uint32_t *__restrict__ packed, const void *__restrict__ absmax_ptr,
+    const float *__restrict__ code, const float *__restrict__ code2,
+    const float *__restrict__ absmax2, const float *__restrict__ offset_ptr,
+    void *__restrict__ out, int64_t chunks, int log2_block, int log2_block2) {
+    __shared__ float lds_code[16];
+    __shared__ float lds_code2[NESTED ? 256 : 1];
+    const int tid = threadIdx.x;
+    if (tid < 16) lds_code[tid] = code[tid];
+    if constexpr (NESTED) lds_code2[tid] = code2[tid];
+    __syncthreads();
+
+    float offset = 0.f;
+    if constexpr (NESTED) offset = *offset_ptr;
+    const int64_t base = (int64_t)blockIdx.x * (kDequantThreads * kChunksPerThread) + tid;
+
+    uint32_t word[kChunksPerThread];
+    float scale[kChunksPerThread];
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+        const int64_t c = base + j * kDequantThreads;
+        if (c < chunks) {
+            word[j] = __builtin_nontemporal_load(packed + c);
+            const int64_t g = (c << 3) >> log2_block;
+            if constexpr (NESTED) {
+                const uint8_t q = static_cast<const uint8_t *>(absmax_ptr)[g];
+                const float decoded = lds_code2[q] * absmax2[g >> log2_block2];
+                scale[j] = decoded + offset;  // separately rounded add (no contraction)
+            } else {
+                scale[j] = static_cast<const float *>(absmax_ptr)[g];
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+        const int64_t c = base + j * kDequantThreads;
+        if (c >= chunks) continue;
+        const uint32_t d = word[j];
+        const float s = scale[j];
+        float v[8];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            v[2 * b] = lds_code[(d >> (8 * b + 4)) & 15u] * s;
+            v[2 * b + 1] = lds_code[(d >> (8 * b)) & 15u] * s;
+        }
+        if constexpr (OUT == CT_F32) {
+            const f32x4 lo = {round_to_storage<STORAGE>(v[0]), round_to_storage<STORAGE>(v[1]),
+                              round_to_storage<STORAGE>(v[2]), round_to_storage<STORAGE>(v[3])};
+            const f32x4 hi = {round_to_storage<STORAGE>(v[4]), round_to_storage<STORAGE>(v[5]),
+                              round_to_storage<STORAGE>(v[6]), round_to_storage<STORAGE>(v[7])};
+            f32x4 *o = static_cast<f32x4 *>(out) + 2 * c;
+            __builtin_nontemporal_store(lo, o);
+            __builtin_nontemporal_store(hi, o + 1);
+        } else {
+            const u32x4 r = {encode_pair<STORAGE, OUT>(v[0], v[1]), encode_pair<STORAGE, OUT>(v[2], v[3]),
+                             encode_pair<STORAGE, OUT>(v[4], v[5]), encode_pair<STORAGE, OUT>(v[6], v[7])};
+            __builtin_nontemporal_store(r, static_cast<u32x4 *>(out) + c);
+        }
+    }
+}
+
+// General path: one lane per packed byte, any N (odd tails included).
+template <bool NESTED, int STORAGE, int OUT>
+__global__ __launch_bounds__(kDequantThreads) void nf4_dequant_any(
+    const uint8_t *__restrict__ packed, const void *__restrict__ absmax_ptr,
+    const float *__restrict__ code, const float *__restrict__ code2,
+    const float *__restrict__ absmax2, const float *__restrict__ offset_ptr,
+    void *__restrict__ out, int64_t n, int log2_block, int log2_block2) {
+    const int64_t p = (int64_t)blockIdx.x * kDequantThreads + threadIdx.x;
+    const int64_t bytes = (n + 1) >> 1;
+    if (p >= bytes) return;
+    const int64_t e = 2 * p;
+    const int64_t g = e >> log2_block;  // 2p and 2p+1 share a block: blocksize is even
+    float s;
+    if constexpr (NESTED) {
+        const uint8_t q = static_cast<const uint8_t *>(absmax_ptr)[g];
+        const float decoded = code2[q] * absmax2[g >> log2_block2];
+        s = decoded + *offset_ptr;
+    } else {
+        s = static_cast<const float *>(absmax_ptr)[g];
+    }
+    const uint8_t byte = packed[p];
+    const float v[2] = {code[byte >> 4] * s, code[byte & 15] * s};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if (e + i >= n) break;
+        const float r = round_to_storage<STORAGE>(v[i]);
+        if constexpr (OUT == CT_F32) static_cast<float *>(out)[e + i] = r;
+        else if constexpr (OUT == CT_BF16) static_cast<uint16_t *>(out)[e + i] = bf16_bits(r);
+        else static_cast<uint16_t *>(out)[e + i] = f16_bits(r);
+    }
+}
+
+int log2_exact(int64_t v) {
+    if (v <= 0 || (v & (v - 1))) return -1;
+    int l = 0;
+    while ((int64_t{1} << l) < v) ++l;
+    return l;
+}
+
+template <bool NESTED, int STORAGE, int OUT>
+hipError_t launch_dequant(const ct_nf4_weight *w, void *out, int64_t n, int lb, int lb2,
+                          bool vec, hipStream_t stream) {
+    if (vec) {
+        const int64_t chunks = n >> 3;
+        const int64_t per_block = kDequantThreads * kChunksPerThread;
+        const int64_t grid = cdiv(chunks, per_block);
+        nf4_dequant_vec<NESTED, STORAGE, OUT><<<dim3((unsigned)grid), dim3(kDequantThreads), 0, stream>>>(
+            reinterpret_cast<const uint32_t *>(w->packed), w->absmax, w->code, w->code2, w->absmax2,
+            w->offset, out, chunks, lb, lb2);
+    } else {
+        const int64_t grid = cdiv((n + 1) >> 1, kDequantThreads);
+        nf4_dequant_any<NESTED, STORAGE, OUT><<<dim3((unsigned)grid), dim3(kDequantThreads), 0, stream>>>(
+            w->packed, w->absmax, w->code, w->code2, w->absmax2, w->offset, out, n, lb, lb2);
+    }
+    return hipGetLastError();
+}
+
+template <bool NESTED, int STORAGE>
+hipError_t dispatch_out(const ct_nf4_weight *w, void *out, int out_dtype, int64_t n, int lb, int lb2,
+                        bool vec, hipStream_t s) {
+    switch (out_dtype) {
+        case CT_BF16: return launch_dequant<NESTED, STORAGE, CT_BF16>(w, out, n, lb, lb2, vec, s);
+        case CT_F16: return launch_dequant<NESTED, STORAGE, CT_F16>(w, out, n, lb, lb2, vec, s);
+        default: return launch_dequant<NESTED, STORAGE, CT_F32>(w, out, n, lb, lb2, vec, s);
+    }
+}
+
+template <bool NESTED>
+hipError_t dispatch_storage(const ct_nf4_weight *w, void *out, int out_dtype, int64_t n, int lb, int lb2,
+                            bool vec, hipStream_t s) {
+    switch (w->storage_dtype) {
+        case CT_BF16: return dispatch_out<NESTED, CT_BF16>(w, out, out_dtype, n, lb, lb2, vec, s);
+        case CT_F16: return dispatch_out<NESTED, CT_F16>(w, out, out_dtype, n, lb, lb2, vec, s);
+        default: return dispatch_out<NESTED, CT_F32>(w, out, out_dtype, n, lb, lb2, vec, s);
+    }
+}
+
+bool valid_dtype(int d) { return d == CT_F32 || d == CT_F16 || d == CT_BF16; }
+
+}  // namespace
+
+// Host-side validation shared with the GEMM entry points.
+int validate_nf4(const ct_nf4_weight *w) {
+    if (!w || !w->packed || !w->absmax || !w->code) return -CT_EINVAL_POINTER;
+    if (w->rows < 0 || w->cols < 0) return -CT_EINVAL_SHAPE;
+    if (!valid_dtype(w->storage_dtype)) return -CT_EINVAL_DTYPE;
+    if (log2_exact(w->blocksize) < 1) return -CT_EINVAL_BLOCKSIZE;
+    if (w->nested) {
+        if (!w->code2 || !w->absmax2 || !w->offset) return -CT_EINVAL_POINTER;
+        if (log2_exact(w->blocksize2) < 0) return -CT_EINVAL_BLOCKSIZE;
+    }
+    return 0;
+}
+
+}  // namespace ct
+
+extern "C" int ct_nf4_dequant(const ct_nf4_weight *w, void *out, int32_t out_dtype, hipStream_t stream) {
+    using namespace ct;
+    int st = validate_nf4(w);
+    if (st) return st;
+    if (!valid_dtype(out_dtype)) return -CT_EINVAL_DTYPE;
+    const int64_t n = w->rows * w->cols;
+    if (n == 0) return 0;
+    if (!out) return -CT_EINVAL_POINTER;
+    const int lb = log2_exact(w->blocksize);
+    const int lb2 = w->nested ? log2_exact(w->blocksize2) : 0;
+    const bool vec = (n % 8 == 0) && w->blocksize >= 8 &&
+                     (reinterpret_cast<uintptr_t>(w->packed) % 4 == 0) &&
+                     (reinterpret_cast<uintptr_t>(out) % 16 == 0);
+    hipError_t e = w->nested ? dispatch_storage<true>(w, out, out_dtype, n, lb, lb2, vec, stream)
+                             : dispatch_storage<false>(w, out, out_dtype, n, lb, lb2, vec, stream);
+    return e == hipSuccess ? 0 : (int)e;
+}

@@ -1,0 +1,165 @@
+/*
+ * C ABI of the MI355X (gfx950) NF4-LoRA projection library `libcausal_tuner_hip.so`.
+ *
+ * Every entry point takes raw device pointers, element counts, leading dimensions and
+ * the caller's HIP stream. The library never allocates or frees device memory and keeps
+ * no pointer, tensor or stream between calls; scratch space for split reductions is a
+ * caller-owned workspace whose size a `*_workspace` query returns. Kernels are enqueued
+ * on `stream` and the call returns without synchronising.
+ *
+ * Status: 0 on success; a negative CT_E* code for an argument error detected on the host
+ * before anything is enqueued; a positive hipError_t if a launch failed. No C++ exception
+ * crosses this boundary. `ct_status_string` names a status.
+ *
+ * Matrices are row-major with unit stride along a row; `ld*` is the distance, in
+ * elements, between consecutive rows. bf16 values are passed as `const void *`.
+ *
+ * Reference interfaces (RealJosephus/causal-tuner, paths under src/causal_tuner/):
+ *   kernels/nf4_cuda.py:9-43    _decode / dequantize_nf4   -> ct_nf4_dequant
+ *   kernels/linear.py:6-13      materialize                -> ct_nf4_dequant
+ *   kernels/linear.py:16-24     accumulate                 -> ct_accumulate
+ *   kernels/linear.py:27-33     forward_linear             -> ct_forward_linear
+ *   kernels/linear.py:36-39     input_gradient             -> ct_input_gradient
+ *   kernels/linear.py:42-44     parameter_gradients        -> ct_parameter_gradients
+ *   kernels/linear.py:84,125    torch.mm(x, a.T, out=xa)   -> ct_gemm (NT, bf16 out)
+ *   kernels/linear.py:124,167   torch.mm(dy, b, out=low)   -> ct_gemm (NN, bf16 out)
+ */
+#ifndef CAUSAL_TUNER_HIP_H
+#define CAUSAL_TUNER_HIP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (the torch dtypes the reference passes through these paths). */
+#define CT_F32  0
+#define CT_F16  1
+#define CT_BF16 2
+
+/* Host-side argument errors (returned negated). */
+#define CT_EINVAL_POINTER   1  /* a required pointer is null or misaligned       */
+#define CT_EINVAL_SHAPE     2  /* a size or leading dimension is out of range    */
+#define CT_EINVAL_DTYPE     3  /* unsupported element type                       */
+#define CT_EINVAL_BLOCKSIZE 4  /* unsupported NF4 block size                     */
+#define CT_EINVAL_WORKSPACE 5  /* workspace missing or smaller than required    */
+
+/*
+ * Frozen NF4 base weight: the fields of a bitsandbytes QuantState that the reference's
+ * decoder reads (kernels/nf4_cuda.py:33-41, kernels/linear.py:8).
+ *   packed     uint8 [ceil(rows*cols/2)]: element 2j in the high nibble of byte j.
+ *   absmax     nested: uint8 [nb] codes into code2; else float32 [nb] block scales.
+ *   code       float32 [16] NF4 code book (state.code).
+ *   code2      float32 [256] second-level code book (state.state2.code), nested only.
+ *   absmax2    float32 [ceil(nb/blocksize2)] (state.state2.absmax), nested only.
+ *   offset     float32 [1] (state.offset), nested only.
+ *   rows, cols the dense shape (state.shape), rows = out features.
+ *   blocksize  first-level block (64..4096, power of two); blocksize2 second level.
+ *   storage_dtype  state.dtype: every decoded value is rounded to it first.
+ * nb = ceil(rows*cols/blocksize).
+ */
+typedef struct ct_nf4_weight {
+    const uint8_t *packed;
+    const void *absmax;
+    const float *code;
+    const float *code2;
+    const float *absmax2;
+    const float *offset;
+    int64_t rows;
+    int64_t cols;
+    int32_t blocksize;
+    int32_t blocksize2;
+    int32_t nested;
+    int32_t storage_dtype;
+} ct_nf4_weight;
+
+int ct_abi_version(void);
+const char *ct_status_string(int status);
+
+/*
+ * Replaces dequantize_nf4 / _decode (kernels/nf4_cuda.py:9-43), the NF4 branch of
+ * materialize (kernels/linear.py:6-13).
+ * out[e] = out_dtype(storage_dtype(code[nibble(e)] * s[e / blocksize])) for e < rows*cols,
+ * with s[g] = code2[absmax[g]] * absmax2[g / blocksize2] + offset (fp32 multiply, then a
+ * separately rounded add) when nested, else s[g] = absmax[g]. Bit-exact to the reference.
+ */
+int ct_nf4_dequant(const ct_nf4_weight *w, void *out, int32_t out_dtype, hipStream_t stream);
+
+/*
+ * Replaces the torch.mm / torch.addmm calls of the projection path (kernels/linear.py:28-33,
+ * 37-39, 84, 124-125, 167). bf16 operands, fp32 accumulation.
+ *   c[m,n] = sum_k A(m,k) B(k,n) (+ bias[n]) (+ c[m,n] if beta)
+ *   A(m,k) = a[m*lda + k]  (trans_a = 0)  or  a[k*lda + m]  (trans_a = 1)
+ *   B(k,n) = b[n*ldb + k]  (trans_b = 1)  or  b[k*ldb + n]  (trans_b = 0)
+ * c_dtype is CT_BF16 (rounded once, RTNE) or CT_F32. bias may be null (bf16 [n]).
+ */
+int ct_gemm(const void *a, int64_t lda, int32_t trans_a,
+            const void *b, int64_t ldb, int32_t trans_b,
+            void *c, int64_t ldc, int32_t c_dtype, const void *bias, int32_t beta,
+            int64_t m, int64_t n, int64_t k, hipStream_t stream);
+
+/*
+ * Replaces forward_linear (kernels/linear.py:27-33):
+ *   xa  = bf16(x a^T)                               [m, r]   (written)
+ *   out = bf16(x w^T + bias + xa b^T)               [m, n]
+ * with the base GEMM and the rank-r epilogue as one contraction over k + r columns.
+ * Exactly one of w_dense (bf16 [n, k]) or w_nf4 (rows n, cols k) is non-null.
+ * x [m, k] (ldx), a bf16 [r, k], b bf16 [n, r], bias bf16 [n] or null, out [m, n] (ldo),
+ * xa bf16 [m, r] contiguous.
+ */
+int ct_forward_linear(const void *x, int64_t ldx,
+                      const void *w_dense, const ct_nf4_weight *w_nf4,
+                      const void *a, const void *b, const void *bias,
+                      void *out, int64_t ldo, void *xa,
+                      int64_t m, int64_t n, int64_t k, int64_t r, hipStream_t stream);
+
+/*
+ * Replaces input_gradient (kernels/linear.py:36-39):
+ *   low = bf16(dy b)                                 [m, r]   (written)
+ *   dx  = bf16(dy w + low a (+ dx if add))           [m, k]
+ * dy [m, n] (lddy), w as in ct_forward_linear, a bf16 [r, k], b bf16 [n, r],
+ * dx [m, k] (lddx), low bf16 [m, r] contiguous.
+ */
+int ct_input_gradient(const void *dy, int64_t lddy,
+                      const void *w_dense, const ct_nf4_weight *w_nf4,
+                      const void *a, const void *b,
+                      void *dx, int64_t lddx, void *low,
+                      int64_t m, int64_t n, int64_t k, int64_t r, int32_t add,
+                      hipStream_t stream);
+
+/*
+ * Replaces parameter_gradients (kernels/linear.py:42-44) with accumulate's fp32 branch
+ * (kernels/linear.py:16-24):
+ *   da = low^T x   (+ da if add)   float32 [r, k]
+ *   db = dy^T xa   (+ db if add)   float32 [n, r]
+ * x [m, k] (ldx), dy [m, n] (lddy), low and xa bf16 [m, r] contiguous. The m-reduction is
+ * split over workgroups and summed in a fixed order, so repeated calls are bit-identical;
+ * add = 0 never reads da/db (NaN-filled storage is ignored).
+ */
+int64_t ct_parameter_gradients_workspace(int64_t m, int64_t n, int64_t k, int64_t r);
+int ct_parameter_gradients(const void *x, int64_t ldx, const void *dy, int64_t lddy,
+                           const void *low, const void *xa, float *da, float *db,
+                           int64_t m, int64_t n, int64_t k, int64_t r, int32_t add,
+                           void *workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Replaces accumulate (kernels/linear.py:16-24) for bf16 operands and a float32 output:
+ *   out[p,q] = sum_j L(p,j) R(j,q) (+ out[p,q] if add)
+ *   L(p,j) = left[p*ldl + j] (trans_l = 0) or left[j*ldl + p] (trans_l = 1)
+ *   R(j,q) = right[j*ldr + q] (trans_r = 0) or right[q*ldr + j] (trans_r = 1)
+ * Deterministic split reduction over j, as ct_parameter_gradients.
+ */
+int64_t ct_accumulate_workspace(int64_t p, int64_t q, int64_t j);
+int ct_accumulate(float *out, int64_t ldo,
+                  const void *left, int64_t ldl, int32_t trans_l,
+                  const void *right, int64_t ldr, int32_t trans_r,
+                  int64_t p, int64_t q, int64_t j, int32_t add,
+                  void *workspace, int64_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CAUSAL_TUNER_HIP_H */

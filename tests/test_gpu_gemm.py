@@ -1,0 +1,102 @@
+"""The bf16 MFMA GEMM family (ct_gemm / ct_accumulate) against float64 products of the same
+bf16 operands. These are the contractions behind torch.mm / torch.addmm in the reference's
+operator layer (kernels/linear.py:16-44)."""
+
+import ctypes
+
+import pytest
+import torch
+
+from causal_tuner.kernels import _native
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(256, 384, 320), (37, 80, 96), (1, 1, 1), (129, 65, 17), (64, 8, 4096), (300, 260, 72)]
+
+
+def _operand(rows, cols, transposed):
+    """A bf16 matrix [rows, cols] stored row-major, or column-major when `transposed`."""
+    if transposed:
+        base = torch.randn(cols, rows, device="cuda").to(torch.bfloat16)
+        return base.T, base, rows
+    base = torch.randn(rows, cols, device="cuda").to(torch.bfloat16)
+    return base, base, cols
+
+
+def _err(got, want):
+    d = (got.double() - want).abs()
+    return float(d.max() / want.abs().max().clamp_min(1e-30)), float((got.double() - want).norm() /
+                                                                     want.norm().clamp_min(1e-30))
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+@pytest.mark.parametrize("trans_a", [0, 1])
+@pytest.mark.parametrize("trans_b", [0, 1])
+@pytest.mark.parametrize("out", [torch.bfloat16, torch.float32])
+def test_gemm_layouts_and_tails(m, n, k, trans_a, trans_b, out):
+    lib = _native.library()
+    a, abase, lda = _operand(m, k, trans_a)
+    b, bbase, ldb = _operand(k, n, not trans_b)   # B(k, n); trans_b=1 stores it as [n, k]
+    bias = (torch.randn(n, device="cuda") * 0.5).to(torch.bfloat16)
+    c = torch.full((m, n), float("nan"), device="cuda", dtype=out)
+    status = lib.ct_gemm(abase.data_ptr(), lda, trans_a, bbase.data_ptr(), ldb, trans_b, c.data_ptr(), n,
+                         _native.dtype_code(out), bias.data_ptr(), 0, m, n, k, _native.stream_of(c))
+    assert status == 0
+    want = a.double() @ b.double() + bias.double()
+    worst, norm = _err(c, want)
+    tol = 8e-3 if out == torch.bfloat16 else 1e-5
+    assert worst <= tol and norm <= tol / 2, (worst, norm)
+    # beta accumulation on top of the previous result, no bias
+    status = lib.ct_gemm(abase.data_ptr(), lda, trans_a, bbase.data_ptr(), ldb, trans_b, c.data_ptr(), n,
+                         _native.dtype_code(out), None, 1, m, n, k, _native.stream_of(c))
+    assert status == 0
+    worst, norm = _err(c, want + a.double() @ b.double())
+    assert worst <= 2 * tol and norm <= tol, (worst, norm)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gradient_first_write_ignores_uninitialized_storage(dtype):
+    """tests/test_kernel_workspaces.py:269-279 (accumulate with add=False ignores NaN)."""
+    if dtype != torch.bfloat16:
+        pytest.skip("the HIP accumulate computes bf16 products (fp32 operands are not on the device path)")
+    from causal_tuner.kernels.linear import accumulate
+    left = torch.randn(19, 37, device="cuda", dtype=dtype)
+    right = torch.randn(37, 23, device="cuda", dtype=dtype)
+    output = torch.full((19, 23), float("nan"), device="cuda")
+    expected = left.float() @ right.float()
+    accumulate(output, left, right, add=False)
+    torch.testing.assert_close(output, expected, rtol=1e-5, atol=1e-5)
+    accumulate(output, left, right, add=True)
+    torch.testing.assert_close(output, expected * 2, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("p,q,j", [(256, 4096, 8192), (4096, 256, 4096), (16, 1024, 512), (11008, 256, 8192)])
+def test_split_reduction_is_deterministic_and_exact_enough(p, q, j):
+    """dA/dB-shaped reductions over many tokens: fixed-order split sums, repeat bit-identical."""
+    from causal_tuner.kernels.linear import accumulate
+    low = torch.randn(j, p, device="cuda").to(torch.bfloat16)    # used transposed, like low.T
+    x = torch.randn(j, q, device="cuda").to(torch.bfloat16)
+    out = torch.full((p, q), float("nan"), device="cuda")
+    accumulate(out, low.T, x, add=False)
+    first = out.clone()
+    accumulate(out, low.T, x, add=False)
+    assert torch.equal(out, first)
+    want = low.double().T @ x.double()
+    worst, norm = _err(first, want)
+    assert worst <= 1e-5 and norm <= 1e-6, (worst, norm)
+    accumulate(out, low.T, x, add=True)
+    worst, _ = _err(out, 2 * want)
+    assert worst <= 1e-5
+
+
+def test_gemm_runs_on_the_callers_stream():
+    lib = _native.library()
+    a = torch.randn(512, 512, device="cuda").to(torch.bfloat16)
+    stream = torch.cuda.Stream()
+    c = torch.empty(512, 512, device="cuda", dtype=torch.float32)
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        assert lib.ct_gemm(a.data_ptr(), 512, 0, a.data_ptr(), 512, 1, c.data_ptr(), 512, _native.CT_F32, None, 0,
+                           512, 512, 512, ctypes.c_void_p(stream.cuda_stream)) == 0
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.testing.assert_close(c, (a.float() @ a.float().T), rtol=1e-4, atol=1e-3)
