@@ -15,12 +15,19 @@ SHAPES = [(256, 384, 320), (37, 80, 96), (1, 1, 1), (129, 65, 17), (64, 8, 4096)
 
 
 def _operand(rows, cols, transposed):
-    """A bf16 matrix [rows, cols] stored row-major, or column-major when `transposed`."""
+    """A bf16 matrix [rows, cols] stored row-major, or column-major when `transposed`.
+
+    Returns (logical view, storage, ld). Element (i, j) lives at i*ld + j (row-major) or
+    j*ld + i (column-major); the storage always covers the largest such offset."""
     if transposed:
         base = torch.randn(cols, rows, device="cuda").to(torch.bfloat16)
-        return base.T, base, rows
+        ld = rows
+        assert base.numel() >= (cols - 1) * ld + rows
+        return base.T, base, ld
     base = torch.randn(rows, cols, device="cuda").to(torch.bfloat16)
-    return base, base, cols
+    ld = cols
+    assert base.numel() >= (rows - 1) * ld + cols
+    return base, base, ld
 
 
 def _err(got, want):
@@ -35,8 +42,10 @@ def _err(got, want):
 @pytest.mark.parametrize("out", [torch.bfloat16, torch.float32])
 def test_gemm_layouts_and_tails(m, n, k, trans_a, trans_b, out):
     lib = _native.library()
-    a, abase, lda = _operand(m, k, trans_a)
-    b, bbase, ldb = _operand(k, n, not trans_b)   # B(k, n); trans_b=1 stores it as [n, k]
+    # A(m, k) = a[m*lda + k] (trans_a=0, row-major) or a[k*lda + m] (trans_a=1, column-major)
+    a, abase, lda = _operand(m, k, bool(trans_a))
+    # B(k, n) = b[k*ldb + n] (trans_b=0, row-major) or b[n*ldb + k] (trans_b=1, column-major)
+    b, bbase, ldb = _operand(k, n, bool(trans_b))
     bias = (torch.randn(n, device="cuda") * 0.5).to(torch.bfloat16)
     c = torch.full((m, n), float("nan"), device="cuda", dtype=out)
     status = lib.ct_gemm(abase.data_ptr(), lda, trans_a, bbase.data_ptr(), ldb, trans_b, c.data_ptr(), n,
