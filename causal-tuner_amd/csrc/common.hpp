@@ -18,6 +18,14 @@ typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
 constexpr int kWave = 64;
 
 // ---------------------------------------------------------------- rounding to storage types
+// Pins v in a VGPR as an fp32 value. Without it the backend folds `fp32 multiply ->
+// half cast` into one v_fma_mixlo_f16 (a single rounding of the exact product), even with
+// contraction off; the reference rounds the product to fp32 first and narrows after.
+__device__ __forceinline__ float as_f32(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // fp32 -> bf16 bits, round to nearest even. On gfx950 the cast lowers to v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint16_t bf16_bits(float v) {
     __bf16 h = (__bf16)v;
@@ -30,7 +38,7 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t bits) {
     return __builtin_bit_cast(float, (uint32_t)bits << 16);
 }
 __device__ __forceinline__ uint16_t f16_bits(float v) {
-    _Float16 h = (_Float16)v;
+    _Float16 h = (_Float16)as_f32(v);
     return __builtin_bit_cast(uint16_t, h);
 }
 __device__ __forceinline__ float f16_to_f32(uint16_t bits) {

@@ -74,8 +74,8 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_vec(
         float v[8];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            v[2 * b] = lds_code[(d >> (8 * b + 4)) & 15u] * s;
-            v[2 * b + 1] = lds_code[(d >> (8 * b)) & 15u] * s;
+            v[2 * b] = as_f32(lds_code[(d >> (8 * b + 4)) & 15u] * s);
+            v[2 * b + 1] = as_f32(lds_code[(d >> (8 * b)) & 15u] * s);
         }
         if constexpr (OUT == CT_F32) {
             const f32x4 lo = {round_to_storage<STORAGE>(v[0]), round_to_storage<STORAGE>(v[1]),
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_any(
         s = static_cast<const float *>(absmax_ptr)[g];
     }
     const uint8_t byte = packed[p];
-    const float v[2] = {code[byte >> 4] * s, code[byte & 15] * s};
+    const float v[2] = {as_f32(code[byte >> 4] * s), as_f32(code[byte & 15] * s)};
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         if (e + i >= n) break;
