@@ -36,6 +36,7 @@ _SIGNATURES = {
     "ct_abi_version": (ctypes.c_int, []),
     "ct_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "ct_nf4_dequant": (ctypes.c_int, [ctypes.POINTER(NF4Weight), _P, _I32, _P]),
+    "ct_nf4_fused_supported": (ctypes.c_int, [ctypes.POINTER(NF4Weight)]),
     "ct_gemm": (ctypes.c_int, [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _P, _I32, _I64, _I64, _I64, _P]),
     "ct_forward_linear": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _P, _I64, _P,
                                          _I64, _I64, _I64, _I64, _P]),

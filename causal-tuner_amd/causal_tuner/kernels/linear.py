@@ -33,14 +33,21 @@ def _unsupported(what, *tensors):
     raise NotImplementedError(f"{what}: the HIP path computes in bfloat16 on the device (got {', '.join(dtypes)})")
 
 
+def _aligned(t):
+    return t.data_ptr() % 16 == 0
+
+
 def _rows(t):
-    """(tensor, leading dimension) of a matrix with unit stride along its rows."""
+    """(tensor, leading dimension) of a matrix with unit stride along its rows; a view whose
+    base is not 16-byte aligned is copied so the kernels can use 16-byte loads."""
     if t.dim() != 2:
         raise ValueError("expected a matrix")
     if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
         if t.shape[0] <= 1 and t.stride(1) == 1:
-            return t, max(t.shape[1], 1)
+            return (t if _aligned(t) else t.clone()), max(t.shape[1], 1)
         t = t.contiguous()
+    if not _aligned(t):
+        t = t.clone()
     return t, t.stride(0)
 
 
@@ -63,7 +70,8 @@ class _Output:
 
     def __init__(self, target):
         self.target = target
-        ok = target.dim() == 2 and target.stride(1) == 1 and target.stride(0) >= target.shape[1]
+        ok = (target.dim() == 2 and target.stride(1) == 1 and target.stride(0) >= target.shape[1]
+              and _aligned(target))
         self.buffer = target if ok else torch.empty(target.shape, dtype=target.dtype, device=target.device)
         self.ld = max(self.buffer.stride(0), self.buffer.shape[1], 1)
 
@@ -223,31 +231,65 @@ def can_fuse(module, x):
 
 
 # ----------------------------------------------------------------------------- grouped autograd
+class _Base:
+    """The frozen base weight of one projection as the HIP GEMMs consume it.
+
+    A packed NF4 weight whose layout the fused loaders accept stays packed: every GEMM
+    decodes it tile by tile into LDS (bit-identical to `materialize`), so no dense copy is
+    written or re-read. Anything else is materialised once, as the reference does
+    (linear.py:70,107).
+    """
+
+    def __init__(self, weight, state, dtype):
+        self.weight, self.state, self.matrix = weight, None, None
+        if state is not None and weight.is_cuda and dtype == torch.bfloat16 and weight.dtype == torch.uint8 \
+                and weight.is_contiguous() and state.quant_type == "nf4":
+            desc = _native.nf4_descriptor(weight, state)
+            if _native.library().ct_nf4_fused_supported(desc) == 1:
+                self.state = state
+        if self.state is None:
+            self.matrix = materialize(weight, state, dtype)
+        self.rows = int(state.shape[0]) if state is not None else len(weight)
+
+    def forward(self, x, a, b, bias, out, xa):
+        if self.state is None:
+            forward_linear(x, self.matrix, a, b, bias=bias, out=out, xa=xa)
+        else:
+            _forward(x, self.weight, self.state, a, b, bias, out, xa)
+
+    def input_gradient(self, dy, a, b, dx, low, add):
+        if self.state is None:
+            input_gradient(dy, self.matrix, a, b, dx, low, add=add)
+        else:
+            _input_gradient(dy, self.weight, self.state, a, b, dx, low, add)
+
+
 class _LoRAGroup(torch.autograd.Function):
-    """Projections sharing one input; saves only the input and parameters (linear.py:59-130)."""
+    """Projections sharing one input; saves only the input and parameters (linear.py:59-130).
+
+    Without an explicit tile the backward runs each projection over all rows at once (the
+    rank-r workspaces are [rows, r]); an explicit tile bounds them as in the reference."""
 
     @staticmethod
     def forward(ctx, x, dtype, tile, states, cosine, sine, head_dim, residual, *parameters):
         ctx.save_for_backward(x, cosine, sine, *parameters)
-        ctx.dtype, ctx.tile, ctx.states = dtype, tile or 4096, states
+        ctx.dtype, ctx.tile, ctx.states = dtype, tile, states
         ctx.head_dim = head_dim
         flat = x.reshape(-1, x.shape[-1]).to(dtype)
         outputs = []
-        rows = min(ctx.tile, len(flat)) if tile else len(flat)
+        step = tile or max(len(flat), 1)
+        rows = min(step, len(flat))
         for index, state in enumerate(states):
             weight, a, b, bias = parameters[index*4:index*4+4]
-            matrix, ac, bc = materialize(weight, state, dtype), a.to(dtype), b.to(dtype)
+            base, ac, bc = _Base(weight, state, dtype), a.to(dtype), b.to(dtype)
             bias = None if bias is None else bias.to(dtype)
-            out = torch.empty((len(flat), len(matrix)), device=x.device, dtype=dtype)
+            out = torch.empty((len(flat), base.rows), device=x.device, dtype=dtype)
             low = torch.empty((rows, len(a)), device=x.device, dtype=dtype)
-            # The untiled path is one fused contraction over all rows; explicit tiles bound
-            # the rank-r workspace to `tile` rows as in the reference.
-            step = tile or max(len(flat), 1)
             for start in range(0, len(flat), step):
                 part = flat[start:start+step]
-                forward_linear(part, matrix, ac, bc, bias=bias, out=out[start:start+step], xa=low[:len(part)])
-            outputs.append(out.reshape(*x.shape[:-1], len(matrix)))
-            del matrix, ac, bc, low
+                base.forward(part, ac, bc, bias, out[start:start+step], low[:len(part)])
+            outputs.append(out.reshape(*x.shape[:-1], base.rows))
+            del base, ac, bc, low
         if head_dim:
             from .core_cuda import rotate_owned_qk
             rotate_owned_qk(outputs[0], outputs[1], cosine, sine, head_dim)
@@ -262,13 +304,14 @@ class _LoRAGroup(torch.autograd.Function):
         dx = torch.empty_like(flat) if ctx.needs_input_grad[0] else None
         if ctx.head_dim:
             cosine, sine = (value.reshape(-1, value.shape[-1]) for value in (cosine, sine))
-        rows = min(ctx.tile, len(flat))
+        step = ctx.tile or max(len(flat), 1)
+        rows = min(step, len(flat))
         rotary = (torch.empty(rows*max(len(b) for b in parameters[2:8:4]), device=x.device, dtype=ctx.dtype)
                   if ctx.head_dim else None)
         results = []
         for index, (state, grad) in enumerate(zip(ctx.states, grad_outputs)):
             weight, a, b, _ = parameters[index*4:index*4+4]
-            matrix = materialize(weight, state, ctx.dtype) if dx is not None else None
+            base = _Base(weight, state, ctx.dtype) if dx is not None else None
             ac, bc = a.to(ctx.dtype), b.to(ctx.dtype)
             dy = grad.reshape(-1, grad.shape[-1]).to(ctx.dtype)
             allocate = torch.empty_like if len(flat) else torch.zeros_like
@@ -276,8 +319,8 @@ class _LoRAGroup(torch.autograd.Function):
             low = torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype)
             xa = torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype)
             rotate = ctx.head_dim and index < 2
-            for start in range(0, len(flat), ctx.tile):
-                stop = start+ctx.tile
+            for start in range(0, len(flat), step):
+                stop = start+step
                 signal = dy[start:stop]
                 if rotate:
                     from .core_cuda import inverse_rope_tile
@@ -285,13 +328,13 @@ class _LoRAGroup(torch.autograd.Function):
                     signal = inverse_rope_tile(signal, cosine[start:stop], sine[start:stop], ctx.head_dim, target)
                 part_low, part_xa = low[:len(signal)], xa[:len(signal)]
                 if dx is not None:
-                    input_gradient(signal, matrix, ac, bc, dx[start:stop], part_low, add=index > 0)
+                    base.input_gradient(signal, ac, bc, dx[start:stop], part_low, index > 0)
                 else:
                     _low_rank(signal, bc, part_low, transpose=False)
                 _low_rank(flat[start:stop], ac, part_xa, transpose=True)
                 parameter_gradients(flat[start:stop], signal, da, db, part_low, part_xa, add=start > 0)
             results.extend((None, da, db, None))
-            del matrix, ac, bc, dy
+            del base, ac, bc, dy
         residual_grad = grad_outputs[0] if ctx.needs_input_grad[7] else None
         return (None if dx is None else dx.reshape_as(x).to(x.dtype), None, None, None, None, None, None,
                 residual_grad, *results)

@@ -1,25 +1,35 @@
 // bf16 MFMA GEMMs for the NF4-LoRA projection path on gfx950.
 //
 // One kernel template serves every contraction of the reference's operator layer
-// (kernels/linear.py:27-44): C[m,n] = sum over one or two K segments of A(m,k) B(k,n),
-// with fp32 accumulation in v_mfma_f32_16x16x32_bf16 and a fused epilogue (bias, beta
-// accumulation, bf16 or fp32 output, or fp32 split partials).
+// (kernels/linear.py:27-44): C[m,n] = sum over one or two reduction segments of
+// A(m,k) B(k,n), fp32 accumulation in v_mfma_f32_16x16x32_bf16, and a fused epilogue
+// (bias, beta accumulation, bf16 or fp32 output, or fp32 split partials).
 //
-// Two segments implement the rank-r LoRA terms as extra reduction columns:
+// Two segments carry the rank-r LoRA terms as extra reduction columns:
 //   forward  out = [x | xa] [w | b]^T      (segment 0: k columns, segment 1: r columns)
 //   backward dx  = [dy | low] [w ; a]      (segment 0: n rows,    segment 1: r rows)
-// so the low-rank epilogue costs no extra pass over the output.
+// so the low-rank term costs no extra pass over the output.
 //
-// Operand staging: each k-tile of both operands is written into LDS as [rows][64] bf16
-// with the reduction dimension contiguous, in 16-byte chunks whose position within a
-// 128-byte row is XORed with a row-dependent swizzle (conflict-free ds_read_b128 for the
-// MFMA fragment reads). A source whose reduction dimension is contiguous in HBM is copied
-// chunk by chunk; a source whose output dimension is contiguous ("k-strided") is loaded
-// as 8x8 blocks of 16-byte rows and transposed in registers with v_perm_b32.
+// Operand sources (how a k-tile reaches LDS):
+//   KC    bf16, reduction dimension contiguous: 16-byte chunks copied as they are;
+//   KS    bf16, output dimension contiguous: 8x8 blocks transposed in registers (v_perm);
+//   NF4   packed NF4 weight [rows, cols] used with its columns as the reduction
+//         dimension (forward: x w^T): 16 packed bytes per lane decode into 32 bf16;
+//   NF4T  the same weight used with its rows as the reduction dimension (dx = dy w):
+//         8 rows x 8 columns per lane, decoded straight into the transposed layout.
+// NF4 decoding follows the reference's rule exactly (kernels/nf4_cuda.py:16-29): the
+// block scale is code2[q] * absmax2 + offset (fp32 multiply, separately rounded add), the
+// value is code[nibble] * scale in fp32, rounded once to bf16; so a fused contraction sees
+// bit-for-bit the weight that the standalone decoder materialises.
 //
-// Fragment mapping: lane l of a wave reads A rows wm0 + 16 f + l%16 and B rows
-// wn0 + (l%16) FN + f for fragment f, so each lane's accumulators for a fixed output row
-// cover FN consecutive columns and the epilogue writes FN-element vectors.
+// LDS holds each k-tile as [rows][64] bf16 (reduction contiguous) in 16-byte chunks whose
+// position in the 128-byte row is XORed with a row-dependent swizzle, so the MFMA fragment
+// reads (ds_read_b128) and the loader writes are free of bank conflicts. Tiles are double
+// buffered: the next tile's global loads are in flight while the current one feeds MFMA.
+//
+// Tile shapes: 256x256 (4 waves of 128x128, accumulators in AGPRs), 128x128 and 64x64.
+// Workgroup ids are remapped so each of the 8 XCDs walks a contiguous, M-grouped range of
+// output tiles: the workgroups that share an L2 also share A and B panels.
 
 #include "common.hpp"
 
@@ -29,15 +39,26 @@ int validate_nf4(const ct_nf4_weight *w);
 
 namespace {
 
-constexpr int kBK = 64;       // reduction columns per k-tile (8 chunks of 8 bf16)
-constexpr int kThreads = 256; // 4 wavefronts per workgroup
-enum { SRC_KC = 0, SRC_KS = 1 };
+constexpr int kBK = 64;        // reduction columns per k-tile (8 chunks of 8 bf16)
+constexpr int kThreads = 256;  // 4 wavefronts per workgroup
+constexpr int kXcds = 8;       // MI355X dispatches workgroups round-robin over 8 XCDs
+constexpr int kGroupM = 8;     // m-tiles per group in the L2-friendly tile order
+
+enum Src { SRC_KC = 0, SRC_KS = 1, SRC_NF4 = 2, SRC_NF4T = 3 };
+
+struct Operand {
+    const void *p;        // bf16 elements, or packed NF4 bytes
+    int64_t ld;           // bf16: row pitch in elements; NF4: columns of the dense weight
+    const void *absmax;   // NF4: u8 codes (nested) or f32 scales
+    const float *absmax2; // NF4 nested: second-level scales
+    const float *offset;  // NF4 nested: scalar offset
+    int32_t lb, lb2;      // NF4: log2 of the first- and second-level block sizes
+    int32_t nested;
+};
 
 struct Segment {
-    const uint16_t *a;  // bf16 bits
-    const uint16_t *b;
-    int64_t lda, ldb;
-    int64_t k;          // reduction extent of this segment
+    Operand a, b;
+    int64_t k;  // reduction extent
 };
 
 struct GemmParams {
@@ -50,116 +71,319 @@ struct GemmParams {
     int64_t tiles_per_split;  // k-tiles handled by one blockIdx.z
     const uint16_t *bias;     // bf16 [n] or null
     int beta;                 // add the existing C
+    int tiles_m, tiles_n;
+    const float *code;        // NF4 code book [16]
+    const float *code2;       // NF4 second-level code book [256]
 };
 
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0, 0, 0, 0); }
 
-// ------------------------------------------------------------------ operand tile loader
-// ROWS: output-dimension extent of the tile. SWZ_DIV: rows that share one swizzle value
-// (1 for A; FN for B, whose fragment rows are strided by FN).
-template <int ROWS, int SRC, bool VEC, int SWZ_DIV>
-struct Loader {
-    static constexpr int kKcPerThread = (ROWS * 8 + kThreads - 1) / kThreads;
-    static constexpr int kRegs = SRC == SRC_KC ? kKcPerThread : 8;
-    uint4 r[kRegs];
+// LDS slot of chunk `chunk` (0..7) of tile row `row`; SWZ_DIV rows share a swizzle value.
+template <int SWZ_DIV>
+__device__ __forceinline__ int slot(int row, int chunk) {
+    return row * 8 + (chunk ^ ((row / SWZ_DIV) & 7));
+}
 
-    __device__ __forceinline__ static int slot(int row, int chunk) {
-        return row * 8 + (chunk ^ ((row / SWZ_DIV) & 7));
+// Eight nibbles of one packed dword -> eight bf16 (element 2j from the high nibble of byte j).
+__device__ __forceinline__ uint4 nf4_decode8(uint32_t d, float s, const float *lds_code) {
+    float v[8];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        v[2 * b] = lds_code[(d >> (8 * b + 4)) & 15u] * s;
+        v[2 * b + 1] = lds_code[(d >> (8 * b)) & 15u] * s;
     }
+    return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                      pack_bf16x2(v[6], v[7]));
+}
 
-    // Source element (row, k) lives at p[row * ld + k] (KC) or p[k * ld + row] (KS).
-    __device__ __forceinline__ void load(const uint16_t *p, int64_t ld, int64_t rows, int64_t kext,
-                                         int64_t r0, int64_t k0, int tid) {
-        if constexpr (SRC == SRC_KC) {
+// ------------------------------------------------------------------ operand tile loaders
+// ROWS: output-dimension extent of the tile. SWZ_DIV: rows that share one swizzle value.
+// load() issues the global reads of k-tile k0 into registers; store() writes the tile to
+// LDS (decoding NF4 on the way).
+template <int SRC, int ROWS, bool VEC, int SWZ_DIV>
+struct Loader;
+
+template <int ROWS, bool VEC, int SWZ_DIV>
+struct Loader<SRC_KC, ROWS, VEC, SWZ_DIV> {
+    static constexpr int kPer = (ROWS * 8 + kThreads - 1) / kThreads;
+    uint4 r[kPer];
+    __device__ __forceinline__ void load(const Operand &o, int64_t rows, int64_t kext, int64_t r0, int64_t k0,
+                                         int tid) {
+        const uint16_t *p = static_cast<const uint16_t *>(o.p);
 #pragma unroll
-            for (int i = 0; i < kKcPerThread; ++i) {
-                const int id = tid + i * kThreads;
-                if (id >= ROWS * 8) break;
-                const int64_t row = r0 + (id >> 3);
-                const int64_t k = k0 + (id & 7) * 8;
-                if constexpr (VEC) {
-                    r[i] = (row < rows && k < kext) ? *reinterpret_cast<const uint4 *>(p + row * ld + k)
-                                                    : zero4();
-                } else {
-                    uint16_t e[8];
+        for (int i = 0; i < kPer; ++i) {
+            const int id = tid + i * kThreads;
+            if (id >= ROWS * 8) break;
+            const int64_t row = r0 + (id >> 3);
+            const int64_t k = k0 + (id & 7) * 8;
+            if constexpr (VEC) {
+                r[i] = (row < rows && k < kext) ? *reinterpret_cast<const uint4 *>(p + row * o.ld + k) : zero4();
+            } else {
+                uint16_t e[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        e[j] = (row < rows && k + j < kext) ? p[row * ld + k + j] : uint16_t(0);
-                    r[i] = __builtin_bit_cast(uint4, e);
-                }
-            }
-        } else {
-            // 8x8 block: k-chunk c = tid % 8, row block rb = tid / 8 (ROWS/8 row blocks).
-            if (tid >= ROWS) return;
-            const int64_t row = r0 + (tid >> 3) * 8;
-            const int64_t kb = k0 + (tid & 7) * 8;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int64_t k = kb + i;
-                if constexpr (VEC) {
-                    r[i] = (k < kext && row < rows) ? *reinterpret_cast<const uint4 *>(p + k * ld + row)
-                                                    : zero4();
-                } else {
-                    uint16_t e[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        e[j] = (k < kext && row + j < rows) ? p[k * ld + row + j] : uint16_t(0);
-                    r[i] = __builtin_bit_cast(uint4, e);
-                }
+                for (int j = 0; j < 8; ++j) e[j] = (row < rows && k + j < kext) ? p[row * o.ld + k + j] : uint16_t(0);
+                r[i] = __builtin_bit_cast(uint4, e);
             }
         }
     }
-
-    __device__ __forceinline__ void store(uint4 *lds, int tid) const {
-        if constexpr (SRC == SRC_KC) {
+    __device__ __forceinline__ void store(uint4 *lds, int tid, const float *, const float *) const {
 #pragma unroll
-            for (int i = 0; i < kKcPerThread; ++i) {
-                const int id = tid + i * kThreads;
-                if (id >= ROWS * 8) break;
-                lds[slot(id >> 3, id & 7)] = r[i];
-            }
-        } else {
-            if (tid >= ROWS) return;
-            uint4 t[8];
-            transpose8x8_b16(r, t);
-            const int row = (tid >> 3) * 8;
-            const int chunk = tid & 7;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) lds[slot(row + j, chunk)] = t[j];
+        for (int i = 0; i < kPer; ++i) {
+            const int id = tid + i * kThreads;
+            if (id >= ROWS * 8) break;
+            lds[slot<SWZ_DIV>(id >> 3, id & 7)] = r[i];
         }
     }
 };
 
-// ------------------------------------------------------------------------- the kernel
-template <int BM, int BN, int WAVES_M, int A_SRC, int B_SRC, bool VEC, int OUT>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p) {
-    constexpr int WAVES_N = 4 / WAVES_M;
-    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;  // wave tile
-    constexpr int FM = WM / 16, FN = WN / 16;             // 16x16 fragments per wave
-    using LA = Loader<BM, A_SRC, VEC, 1>;
-    using LB = Loader<BN, B_SRC, VEC, FN>;
+template <int ROWS, bool VEC, int SWZ_DIV>
+struct Loader<SRC_KS, ROWS, VEC, SWZ_DIV> {
+    // ROWS/8 row blocks x 8 k-chunks = ROWS blocks of 8x8, at most one per lane.
+    uint4 r[8];
+    __device__ __forceinline__ void load(const Operand &o, int64_t rows, int64_t kext, int64_t r0, int64_t k0,
+                                         int tid) {
+        if (tid >= ROWS) return;
+        const uint16_t *p = static_cast<const uint16_t *>(o.p);
+        const int64_t row = r0 + (tid % (ROWS / 8)) * 8;
+        const int64_t kb = k0 + (tid / (ROWS / 8)) * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int64_t k = kb + i;
+            if constexpr (VEC) {
+                r[i] = (k < kext && row < rows) ? *reinterpret_cast<const uint4 *>(p + k * o.ld + row) : zero4();
+            } else {
+                uint16_t e[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) e[j] = (k < kext && row + j < rows) ? p[k * o.ld + row + j] : uint16_t(0);
+                r[i] = __builtin_bit_cast(uint4, e);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(uint4 *lds, int tid, const float *, const float *) const {
+        if (tid >= ROWS) return;
+        uint4 t[8];
+        transpose8x8_b16(r, t);
+        const int row = (tid % (ROWS / 8)) * 8;
+        const int chunk = tid / (ROWS / 8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) lds[slot<SWZ_DIV>(row + j, chunk)] = t[j];
+    }
+};
 
-    __shared__ uint4 lds[2][(BM + BN) * 8];
+// NF4 weight [rows][cols], reduction along cols (forward: x w^T). One unit = 32 elements
+// of one row: 16 packed bytes inside one first-level block (blocksize >= 32, cols % 32 == 0).
+// load() fetches the packed bytes and the block's scale code; store() decodes.
+template <int ROWS, bool VEC, int SWZ_DIV>
+struct Loader<SRC_NF4, ROWS, VEC, SWZ_DIV> {
+    static constexpr int kUnits = ROWS * 2;
+    static constexpr int kPer = (kUnits + kThreads - 1) / kThreads;
+    uint4 q[kPer];
+    float a2[kPer];     // nested: absmax2 of the block's group; plain: the block scale
+    uint32_t qa[kPer];  // nested: the block's u8 scale code; 256 marks an empty unit
+    __device__ __forceinline__ void load(const Operand &o, int64_t rows, int64_t kext, int64_t r0, int64_t k0,
+                                         int tid) {
+        const uint8_t *packed = static_cast<const uint8_t *>(o.p);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int id = tid + i * kThreads;
+            if (id >= kUnits) break;
+            const int64_t row = r0 + (id >> 1);
+            const int64_t k = k0 + (id & 1) * 32;
+            if (row < rows && k < kext) {
+                const int64_t e = row * o.ld + k;
+                const int64_t g = e >> o.lb;
+                q[i] = *reinterpret_cast<const uint4 *>(packed + (e >> 1));
+                if (o.nested) {
+                    qa[i] = static_cast<const uint8_t *>(o.absmax)[g];
+                    a2[i] = o.absmax2[g >> o.lb2];
+                } else {
+                    qa[i] = 0;
+                    a2[i] = static_cast<const float *>(o.absmax)[g];
+                }
+            } else {
+                q[i] = zero4();
+                qa[i] = 256;
+                a2[i] = 0.f;
+            }
+        }
+    }
+    __device__ __forceinline__ void store(uint4 *lds, int tid, const float *lcode, const float *lcode2,
+                                          int nested, float offset) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int id = tid + i * kThreads;
+            if (id >= kUnits) break;
+            float s = a2[i];
+            if (nested) s = qa[i] < 256 ? lcode2[qa[i]] * a2[i] + offset : 0.f;
+            const int row = id >> 1, c0 = (id & 1) * 4;
+            lds[slot<SWZ_DIV>(row, c0 + 0)] = nf4_decode8(q[i].x, s, lcode);
+            lds[slot<SWZ_DIV>(row, c0 + 1)] = nf4_decode8(q[i].y, s, lcode);
+            lds[slot<SWZ_DIV>(row, c0 + 2)] = nf4_decode8(q[i].z, s, lcode);
+            lds[slot<SWZ_DIV>(row, c0 + 3)] = nf4_decode8(q[i].w, s, lcode);
+        }
+    }
+};
+
+// NF4 weight [rows][cols], reduction along rows (the transposed use in dx = dy w). One
+// unit = 8 weight rows x 8 weight columns (one packed dword per row), at most one per lane;
+// the decoded values are written straight into the reduction-contiguous LDS layout.
+template <int ROWS, bool VEC, int SWZ_DIV>
+struct Loader<SRC_NF4T, ROWS, VEC, SWZ_DIV> {
+    static constexpr int kCB = ROWS / 8;  // 8-column blocks across the tile
+    uint32_t d[8];
+    float a2[8];
+    uint32_t qa[8];
+    __device__ __forceinline__ void load(const Operand &o, int64_t rows, int64_t kext, int64_t r0, int64_t k0,
+                                         int tid) {
+        if (tid >= 8 * kCB) return;
+        const uint8_t *packed = static_cast<const uint8_t *>(o.p);
+        const int64_t col = r0 + (tid % kCB) * 8;
+        const int64_t wrow0 = k0 + (tid / kCB) * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int64_t wrow = wrow0 + i;
+            if (wrow < kext && col < rows) {
+                const int64_t e = wrow * o.ld + col;
+                const int64_t g = e >> o.lb;
+                d[i] = *reinterpret_cast<const uint32_t *>(packed + (e >> 1));
+                if (o.nested) {
+                    qa[i] = static_cast<const uint8_t *>(o.absmax)[g];
+                    a2[i] = o.absmax2[g >> o.lb2];
+                } else {
+                    qa[i] = 0;
+                    a2[i] = static_cast<const float *>(o.absmax)[g];
+                }
+            } else {
+                d[i] = 0;
+                qa[i] = 256;
+                a2[i] = 0.f;
+            }
+        }
+    }
+    __device__ __forceinline__ void store(uint4 *lds, int tid, const float *lcode, const float *lcode2,
+                                          int nested, float offset) const {
+        if (tid >= 8 * kCB) return;
+        float s[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            s[i] = a2[i];
+            if (nested) s[i] = qa[i] < 256 ? lcode2[qa[i]] * a2[i] + offset : 0.f;
+        }
+        const int col = (tid % kCB) * 8;
+        const int chunk = tid / kCB;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // column j of the 8x8 unit: element j of each row's dword (high nibble first)
+            const int shift = (j & 1) ? 8 * (j >> 1) : 8 * (j >> 1) + 4;
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = lcode[(d[i] >> shift) & 15u] * s[i];
+            lds[slot<SWZ_DIV>(col + j, chunk)] = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                            pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+        }
+    }
+};
+
+// Dense loaders ignore the NF4 tables.
+template <int SRC>
+constexpr bool is_nf4() { return SRC == SRC_NF4 || SRC == SRC_NF4T; }
+
+template <class L, int SRC>
+__device__ __forceinline__ void store_tile(const L &l, uint4 *lds, int tid, const float *lcode,
+                                           const float *lcode2, int nested, float offset) {
+    if constexpr (is_nf4<SRC>()) l.store(lds, tid, lcode, lcode2, nested, offset);
+    else l.store(lds, tid, lcode, lcode2);
+}
+
+// ------------------------------------------------------------------ one reduction segment
+template <int BM, int BN, int SA, int SB, bool VEC>
+struct SegmentRunner {
+    static constexpr int WM = BM / 2, WN = BN / 2;  // 2 x 2 waves
+    static constexpr int FM = WM / 16, FN = WN / 16;
+    static constexpr int kStage = (BM + BN) * 8;    // uint4 slots per pipeline stage
+
+    __device__ __forceinline__ static void run(const Segment &sg, int64_t m, int64_t n, int64_t m0, int64_t n0,
+                                               int64_t tbeg, int64_t tend, f32x4 (&acc)[FM][FN], uint4 *lds,
+                                               const float *lcode, const float *lcode2, int tid, int wm0,
+                                               int wn0) {
+        if (tbeg >= tend) return;
+        const int lane = tid & 63;
+        Loader<SA, BM, VEC, 1> la;
+        Loader<SB, BN, VEC, FN> lb;
+        const float off_a = (is_nf4<SA>() && sg.a.nested) ? *sg.a.offset : 0.f;
+        const float off_b = (is_nf4<SB>() && sg.b.nested) ? *sg.b.offset : 0.f;
+        la.load(sg.a, m, sg.k, m0, tbeg * kBK, tid);
+        lb.load(sg.b, n, sg.k, n0, tbeg * kBK, tid);
+        __syncthreads();  // every wave is done with the buffers of a previous segment
+        store_tile<decltype(la), SA>(la, lds, tid, lcode, lcode2, sg.a.nested, off_a);
+        store_tile<decltype(lb), SB>(lb, lds + BM * 8, tid, lcode, lcode2, sg.b.nested, off_b);
+        __syncthreads();
+        for (int64_t t = tbeg; t < tend; ++t) {
+            const int buf = (int)((t - tbeg) & 1);
+            const bool more = t + 1 < tend;
+            if (more) {
+                la.load(sg.a, m, sg.k, m0, (t + 1) * kBK, tid);
+                lb.load(sg.b, n, sg.k, n0, (t + 1) * kBK, tid);
+            }
+            const uint4 *sa = lds + buf * kStage;
+            const uint4 *sb = sa + BM * 8;
+#pragma unroll
+            for (int ks = 0; ks < kBK / 32; ++ks) {
+                const int chunk = ks * 4 + (lane >> 4);
+                uint4 af[FM], bf[FN];
+#pragma unroll
+                for (int i = 0; i < FM; ++i) af[i] = sa[slot<1>(wm0 + i * 16 + (lane & 15), chunk)];
+#pragma unroll
+                for (int j = 0; j < FN; ++j) bf[j] = sb[slot<FN>(wn0 + (lane & 15) * FN + j, chunk)];
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the next tile's stores after the MFMA block
+            if (more) {
+                uint4 *next = lds + (buf ^ 1) * kStage;
+                store_tile<decltype(la), SA>(la, next, tid, lcode, lcode2, sg.a.nested, off_a);
+                store_tile<decltype(lb), SB>(lb, next + BM * 8, tid, lcode, lcode2, sg.b.nested, off_b);
+            }
+            __syncthreads();
+        }
+    }
+};
+
+// ------------------------------------------------------------------------- the kernel body
+template <int BM, int BN, int A0, int B0, int A1, int B1, bool VEC, int OUT>
+__device__ __forceinline__ void gemm_body(const GemmParams &p) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 16, FN = WN / 16;
+    constexpr bool kNF4 = is_nf4<A0>() || is_nf4<B0>() || is_nf4<A1>() || is_nf4<B1>();
+    __shared__ uint4 lds[2 * (BM + BN) * 8];
+    __shared__ float lcode[kNF4 ? 16 : 1];
+    __shared__ float lcode2[kNF4 ? 256 : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm0 = (wave % WAVES_M) * WM, wn0 = (wave / WAVES_M) * WN;
-    const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+    const int wm0 = (wave & 1) * WM, wn0 = (wave >> 1) * WN;
 
-    const int64_t t0 = cdiv(p.seg[0].k, kBK);
-    const int64_t total = t0 + (p.nseg > 1 ? cdiv(p.seg[1].k, kBK) : 0);
-    const int64_t tbeg = (int64_t)blockIdx.z * p.tiles_per_split;
-    const int64_t tend = tbeg + p.tiles_per_split < total ? tbeg + p.tiles_per_split : total;
+    // Tile order: contiguous ranges per XCD, M-grouped inside a range.
+    const int tiles = p.tiles_m * p.tiles_n;
+    const int pid = blockIdx.x;
+    const int xcd = pid % kXcds, local = pid / kXcds;
+    const int per = (tiles + kXcds - 1) / kXcds;
+    const int tall = tiles % kXcds == 0 ? kXcds : tiles % kXcds;
+    const int rid = xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
+    const int group = rid / (kGroupM * p.tiles_n);
+    const int first_m = group * kGroupM;
+    const int gsize = p.tiles_m - first_m < kGroupM ? p.tiles_m - first_m : kGroupM;
+    const int tm = first_m + (rid % (kGroupM * p.tiles_n)) % gsize;
+    const int tn = (rid % (kGroupM * p.tiles_n)) / gsize;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
 
-    LA la;
-    LB lb;
-    auto fetch = [&](int64_t t) {
-        const int s = t < t0 ? 0 : 1;
-        const int64_t k0 = (s == 0 ? t : t - t0) * kBK;
-        const Segment &g = p.seg[s];
-        la.load(g.a, g.lda, p.m, g.k, m0, k0, tid);
-        lb.load(g.b, g.ldb, p.n, g.k, n0, k0, tid);
-    };
+    if constexpr (kNF4) {
+        if (tid < 16) lcode[tid] = p.code[tid];
+        if (p.code2) lcode2[tid] = p.code2[tid];
+        // made visible by the barrier that precedes the first tile store
+    }
 
     f32x4 acc[FM][FN];
 #pragma unroll
@@ -167,43 +391,27 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    if (tbeg < tend) {
-        fetch(tbeg);
-        la.store(lds[0], tid);
-        lb.store(lds[0] + BM * 8, tid);
-        __syncthreads();
-        for (int64_t t = tbeg; t < tend; ++t) {
-            const int buf = (int)((t - tbeg) & 1);
-            if (t + 1 < tend) fetch(t + 1);
-            const uint4 *sa = lds[buf];
-            const uint4 *sb = lds[buf] + BM * 8;
-#pragma unroll
-            for (int ks = 0; ks < kBK / 32; ++ks) {
-                const int chunk = ks * 4 + (lane >> 4);
-                uint4 af[FM], bf[FN];
-#pragma unroll
-                for (int i = 0; i < FM; ++i) af[i] = sa[LA::slot(wm0 + i * 16 + (lane & 15), chunk)];
-#pragma unroll
-                for (int j = 0; j < FN; ++j) bf[j] = sb[LB::slot(wn0 + (lane & 15) * FN + j, chunk)];
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
-            }
-            if (t + 1 < tend) {
-                la.store(lds[buf ^ 1], tid);
-                lb.store(lds[buf ^ 1] + BM * 8, tid);
-            }
-            __syncthreads();
-        }
+    const int64_t t0 = cdiv(p.seg[0].k, kBK);
+    const int64_t t1 = p.nseg > 1 ? cdiv(p.seg[1].k, kBK) : 0;
+    const int64_t tbeg = (int64_t)blockIdx.z * p.tiles_per_split;
+    const int64_t tend = tbeg + p.tiles_per_split < t0 + t1 ? tbeg + p.tiles_per_split : t0 + t1;
+    {
+        const int64_t b = tbeg, e = tend < t0 ? tend : t0;
+        SegmentRunner<BM, BN, A0, B0, VEC>::run(p.seg[0], p.m, p.n, m0, n0, b, e, acc, lds, lcode, lcode2, tid,
+                                                wm0, wn0);
+    }
+    if (t1 > 0) {
+        const int64_t b = tbeg > t0 ? tbeg - t0 : 0, e = tend - t0;
+        SegmentRunner<BM, BN, A1, B1, VEC>::run(p.seg[1], p.m, p.n, m0, n0, b, e, acc, lds, lcode, lcode2, tid,
+                                                wm0, wn0);
     }
 
     // ------------------------------------------------------------------ epilogue
+    // Lane l holds rows wm0 + 16 i + 4 (l / 16) + e and columns wn0 + FN (l % 16) + j.
     const int64_t col = n0 + wn0 + (lane & 15) * FN;
     float bias[FN];
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-        bias[j] = (p.bias && col + j < p.n) ? bf16_to_f32(p.bias[col + j]) : 0.f;
+    for (int j = 0; j < FN; ++j) bias[j] = (p.bias && col + j < p.n) ? bf16_to_f32(p.bias[col + j]) : 0.f;
     const bool full = col + FN <= p.n;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
@@ -216,10 +424,19 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p) {
             for (int j = 0; j < FN; ++j) v[j] = acc[i][j][e] + bias[j];
             if constexpr (OUT == CT_F32) {
                 float *c = static_cast<float *>(p.c) + (int64_t)blockIdx.z * p.split_stride + row * p.ldc + col;
+                if (VEC && full && FN % 4 == 0) {
 #pragma unroll
-                for (int j = 0; j < FN; ++j) {
-                    if (!full && col + j >= p.n) break;
-                    c[j] = p.beta ? v[j] + c[j] : v[j];
+                    for (int j = 0; j < FN; j += 4) {
+                        f32x4 w = {v[j], v[j + 1], v[j + 2], v[j + 3]};
+                        if (p.beta) w += *reinterpret_cast<const f32x4 *>(c + j);
+                        *reinterpret_cast<f32x4 *>(c + j) = w;
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+                        if (!full && col + j >= p.n) break;
+                        c[j] = p.beta ? v[j] + c[j] : v[j];
+                    }
                 }
             } else {
                 uint16_t *c = static_cast<uint16_t *>(p.c) + row * p.ldc + col;
@@ -228,11 +445,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p) {
                     for (int j = 0; j < FN; ++j)
                         if (full || col + j < p.n) v[j] = v[j] + bf16_to_f32(c[j]);
                 }
-                if (VEC && full && FN == 4) {
-                    uint2 w;
-                    w.x = pack_bf16x2(v[0], v[1]);
-                    w.y = pack_bf16x2(v[2], v[3]);
-                    *reinterpret_cast<uint2 *>(c) = w;
+                if (VEC && full && FN >= 2) {
+                    uint32_t w[FN / 2];
+#pragma unroll
+                    for (int j = 0; j < FN / 2; ++j) w[j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
+                    if constexpr (FN == 8) *reinterpret_cast<uint4 *>(c) = make_uint4(w[0], w[1], w[2], w[3]);
+                    else if constexpr (FN == 4) *reinterpret_cast<uint2 *>(c) = make_uint2(w[0], w[1]);
+                    else *reinterpret_cast<uint32_t *>(c) = w[0];
                 } else {
 #pragma unroll
                     for (int j = 0; j < FN; ++j) {
@@ -243,6 +462,18 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p) {
             }
         }
     }
+}
+
+// 256x256 tiles: one workgroup per CU, 512 registers per lane (accumulators in AGPRs).
+template <int A0, int B0, int A1, int B1, bool VEC, int OUT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_big(
+    const GemmParams p) {
+    gemm_body<256, 256, A0, B0, A1, B1, VEC, OUT>(p);
+}
+
+template <int BM, int BN, int A0, int B0, int A1, int B1, bool VEC, int OUT>
+__global__ __launch_bounds__(kThreads) void gemm_small(const GemmParams p) {
+    gemm_body<BM, BN, A0, B0, A1, B1, VEC, OUT>(p);
 }
 
 // Deterministic reduction of fp32 split partials: out = sum_z ws[z] (+ out), in z order.
@@ -265,15 +496,20 @@ __global__ __launch_bounds__(256) void reduce_splits(const float *__restrict__ w
 }
 
 // ------------------------------------------------------------------------ host side
+enum Tile { TILE_256 = 0, TILE_128 = 1, TILE_64 = 2 };
+constexpr int kTileEdge[3] = {256, 128, 64};
+
 struct Problem {
     GemmParams p;
-    int a_src, b_src;
+    int src[4];   // A0, B0, A1, B1
     int out;      // CT_BF16 or CT_F32
     bool vec;
     int splits;
+    int tile;     // forced tile, or -1 to choose
 };
 
 bool aligned16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
+constexpr bool is_nf4_host(int src) { return src == SRC_NF4 || src == SRC_NF4T; }
 
 // Vector (16-byte) operand access needs aligned bases, leading dimensions that are
 // multiples of 8 elements, and 8-multiple extents along each contiguous dimension.
@@ -281,87 +517,126 @@ bool vec_ok(const Problem &pr) {
     const GemmParams &p = pr.p;
     for (int s = 0; s < p.nseg; ++s) {
         const Segment &g = p.seg[s];
-        if (!aligned16(g.a) || !aligned16(g.b) || g.lda % 8 || g.ldb % 8) return false;
+        const int sa = pr.src[2 * s], sb = pr.src[2 * s + 1];
         if (g.k % 8) return false;
-        if (pr.a_src == SRC_KS && p.m % 8) return false;
-        if (pr.b_src == SRC_KS && p.n % 8) return false;
+        if (!is_nf4_host(sa) && (!aligned16(g.a.p) || g.a.ld % 8)) return false;
+        if (!is_nf4_host(sb) && (!aligned16(g.b.p) || g.b.ld % 8)) return false;
+        if (sa == SRC_KS && p.m % 8) return false;
+        if (sb == SRC_KS && p.n % 8) return false;
     }
-    if (pr.out == CT_BF16 && (!aligned16(p.c) || p.ldc % 8)) return false;
+    if (!aligned16(p.c) || p.ldc % 8) return false;
     return true;
 }
 
-template <int BM, int BN, int WAVES_M, int A_SRC, int B_SRC, bool VEC, int OUT>
-hipError_t launch_cfg(const GemmParams &p, int splits, hipStream_t s) {
-    dim3 grid((unsigned)cdiv(p.n, BN), (unsigned)cdiv(p.m, BM), (unsigned)splits);
-    gemm_kernel<BM, BN, WAVES_M, A_SRC, B_SRC, VEC, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
+// Largest tile that still yields about one workgroup per CU (256 CUs).
+int choose_tile(int64_t m, int64_t n, int splits) {
+    for (int t = TILE_256; t < TILE_64; ++t) {
+        const int64_t e = kTileEdge[t];
+        if (cdiv(m, e) * cdiv(n, e) * splits >= 256) return t;
+    }
+    return TILE_64;
+}
+
+template <int A0, int B0, int A1, int B1, bool VEC, int OUT>
+hipError_t launch_cfg(const GemmParams &p0, int tile, int splits, hipStream_t s) {
+    GemmParams p = p0;
+    const int e = kTileEdge[tile];
+    p.tiles_m = (int)cdiv(p.m, e);
+    p.tiles_n = (int)cdiv(p.n, e);
+    dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)splits);
+    if (tile == TILE_256) gemm_big<A0, B0, A1, B1, VEC, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
+    else if (tile == TILE_128) gemm_small<128, 128, A0, B0, A1, B1, VEC, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
+    else gemm_small<64, 64, A0, B0, A1, B1, VEC, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
     return hipGetLastError();
 }
 
-template <int A_SRC, int B_SRC, bool VEC, int OUT>
-hipError_t launch_tiles(const GemmParams &p, int splits, bool small, hipStream_t s) {
-    if (small) return launch_cfg<64, 64, 2, A_SRC, B_SRC, VEC, OUT>(p, splits, s);
-    return launch_cfg<128, 128, 2, A_SRC, B_SRC, VEC, OUT>(p, splits, s);
-}
-
-template <int A_SRC, int B_SRC>
-hipError_t launch_layout(const GemmParams &p, int splits, bool small, bool vec, int out, hipStream_t s) {
-    if (vec) {
-        return out == CT_F32 ? launch_tiles<A_SRC, B_SRC, true, CT_F32>(p, splits, small, s)
-                             : launch_tiles<A_SRC, B_SRC, true, CT_BF16>(p, splits, small, s);
+template <int A0, int B0, int A1, int B1>
+hipError_t launch_vec_out(const Problem &pr, int tile, hipStream_t s) {
+    if (pr.vec) {
+        return pr.out == CT_F32 ? launch_cfg<A0, B0, A1, B1, true, CT_F32>(pr.p, tile, pr.splits, s)
+                                : launch_cfg<A0, B0, A1, B1, true, CT_BF16>(pr.p, tile, pr.splits, s);
     }
-    return out == CT_F32 ? launch_tiles<A_SRC, B_SRC, false, CT_F32>(p, splits, small, s)
-                         : launch_tiles<A_SRC, B_SRC, false, CT_BF16>(p, splits, small, s);
+    return pr.out == CT_F32 ? launch_cfg<A0, B0, A1, B1, false, CT_F32>(pr.p, tile, pr.splits, s)
+                            : launch_cfg<A0, B0, A1, B1, false, CT_BF16>(pr.p, tile, pr.splits, s);
 }
 
 int64_t total_tiles(const GemmParams &p) {
     return cdiv(p.seg[0].k, kBK) + (p.nseg > 1 ? cdiv(p.seg[1].k, kBK) : 0);
 }
 
-// Small problems (fewer than ~2 waves of 128x128 tiles over 256 CUs) use 64x64 tiles.
-bool use_small_tiles(int64_t m, int64_t n) { return cdiv(m, 128) * cdiv(n, 128) < 512; }
+#define CT_LAYOUT(a0, b0, a1, b1) \
+    (((a0) << 12) | ((b0) << 8) | ((a1) << 4) | (b1))
 
 hipError_t run(Problem &pr, hipStream_t s) {
     GemmParams &p = pr.p;
     if (p.m == 0 || p.n == 0) return hipSuccess;
-    const bool small = use_small_tiles(p.m, p.n);
+    if (p.nseg == 1) {
+        pr.src[2] = pr.src[0];
+        pr.src[3] = pr.src[1];
+    }
+    const int tile = pr.tile >= 0 ? pr.tile : choose_tile(p.m, p.n, pr.splits);
     const int64_t tiles = total_tiles(p);
     p.tiles_per_split = cdiv(tiles > 0 ? tiles : 1, pr.splits);
-    const int a = pr.a_src, b = pr.b_src;
-    if (a == SRC_KC && b == SRC_KC) return launch_layout<SRC_KC, SRC_KC>(p, pr.splits, small, pr.vec, pr.out, s);
-    if (a == SRC_KC && b == SRC_KS) return launch_layout<SRC_KC, SRC_KS>(p, pr.splits, small, pr.vec, pr.out, s);
-    if (a == SRC_KS && b == SRC_KS) return launch_layout<SRC_KS, SRC_KS>(p, pr.splits, small, pr.vec, pr.out, s);
-    return launch_layout<SRC_KS, SRC_KC>(p, pr.splits, small, pr.vec, pr.out, s);
+    const bool nf4 = is_nf4_host(pr.src[0]) || is_nf4_host(pr.src[1]);
+    if (nf4 && pr.out != CT_BF16) return hipErrorInvalidValue;
+    switch (CT_LAYOUT(pr.src[0], pr.src[1], pr.src[2], pr.src[3])) {
+        case CT_LAYOUT(SRC_KC, SRC_KC, SRC_KC, SRC_KC):
+            return launch_vec_out<SRC_KC, SRC_KC, SRC_KC, SRC_KC>(pr, tile, s);
+        case CT_LAYOUT(SRC_KC, SRC_KS, SRC_KC, SRC_KS):
+            return launch_vec_out<SRC_KC, SRC_KS, SRC_KC, SRC_KS>(pr, tile, s);
+        case CT_LAYOUT(SRC_KS, SRC_KS, SRC_KS, SRC_KS):
+            return launch_vec_out<SRC_KS, SRC_KS, SRC_KS, SRC_KS>(pr, tile, s);
+        case CT_LAYOUT(SRC_KS, SRC_KC, SRC_KS, SRC_KC):
+            return launch_vec_out<SRC_KS, SRC_KC, SRC_KS, SRC_KC>(pr, tile, s);
+        // NF4 loaders keep their own alignment (checked by nf4_fusable); VEC covers the
+        // dense operands and the output.
+        case CT_LAYOUT(SRC_KC, SRC_NF4, SRC_KC, SRC_KC):
+            return pr.vec ? launch_cfg<SRC_KC, SRC_NF4, SRC_KC, SRC_KC, true, CT_BF16>(p, tile, pr.splits, s)
+                          : launch_cfg<SRC_KC, SRC_NF4, SRC_KC, SRC_KC, false, CT_BF16>(p, tile, pr.splits, s);
+        case CT_LAYOUT(SRC_KC, SRC_NF4T, SRC_KC, SRC_KS):
+            return pr.vec ? launch_cfg<SRC_KC, SRC_NF4T, SRC_KC, SRC_KS, true, CT_BF16>(p, tile, pr.splits, s)
+                          : launch_cfg<SRC_KC, SRC_NF4T, SRC_KC, SRC_KS, false, CT_BF16>(p, tile, pr.splits, s);
+        default:
+            return hipErrorInvalidValue;
+    }
 }
 
-// Split count for a reduction-heavy GEMM with a small output (dA, dB): enough
-// workgroups to cover the 256 CUs about twice, at least 4 k-tiles per split.
-int choose_splits(int64_t m, int64_t n, int64_t kred) {
-    const int64_t tiles_out = use_small_tiles(m, n) ? cdiv(m, 64) * cdiv(n, 64) : cdiv(m, 128) * cdiv(n, 128);
+// Tile and split count for a reduction-heavy GEMM with a small output (dA, dB): enough
+// workgroups for about one per CU, at least 8 k-tiles per split, at most 32 splits.
+void choose_reduction(int64_t m, int64_t n, int64_t kred, int *tile, int *splits) {
+    *tile = (m >= 128 && n >= 128) ? TILE_128 : TILE_64;
+    const int64_t e = kTileEdge[*tile];
+    const int64_t tiles_out = cdiv(m, e) * cdiv(n, e);
     const int64_t ktiles = cdiv(kred, kBK);
-    int64_t s = cdiv(512, tiles_out > 0 ? tiles_out : 1);
-    const int64_t cap = ktiles / 4 > 1 ? ktiles / 4 : 1;
+    int64_t s = cdiv(256, tiles_out > 0 ? tiles_out : 1);
+    const int64_t cap = ktiles / 8 > 1 ? ktiles / 8 : 1;
     if (s > cap) s = cap;
     if (s > 32) s = 32;
-    return (int)(s < 1 ? 1 : s);
+    *splits = (int)(s < 1 ? 1 : s);
 }
 
 int64_t split_workspace_bytes(int64_t m, int64_t n, int64_t kred) {
-    const int s = choose_splits(m, n, kred);
+    int tile, s;
+    choose_reduction(m, n, kred, &tile, &s);
     return s > 1 ? (int64_t)s * m * n * (int64_t)sizeof(float) : 0;
 }
 
-// out (fp32 or bf16) = sum_k A B (+ out) through split partials in ws when profitable.
+// out (fp32 or bf16) = sum_k A B (+ out), through fixed-order split partials in ws when
+// the output alone cannot fill the GPU.
 hipError_t run_reduction(Problem pr, void *out, int64_t ldo, int add, void *ws, int64_t ws_bytes,
                          hipStream_t s, int *status) {
     GemmParams &p = pr.p;
     const int64_t kred = p.seg[0].k;
-    const int splits = choose_splits(p.m, p.n, kred);
+    int tile, splits;
+    choose_reduction(p.m, p.n, kred, &tile, &splits);
     *status = 0;
+    pr.tile = tile;
     if (splits <= 1) {
         pr.splits = 1;
         p.c = out;
         p.ldc = ldo;
         p.beta = add;
+        pr.vec = pr.vec && aligned16(out) && ldo % 8 == 0;
         return run(pr, s);
     }
     const int64_t need = (int64_t)splits * p.m * p.n * (int64_t)sizeof(float);
@@ -377,6 +652,7 @@ hipError_t run_reduction(Problem pr, void *out, int64_t ldo, int add, void *ws, 
     p.split_stride = p.m * p.n;
     p.beta = 0;
     p.bias = nullptr;
+    pr.vec = pr.vec && aligned16(ws) && p.n % 8 == 0;
     hipError_t e = run(pr, s);
     if (e != hipSuccess) return e;
     const int64_t count = p.m * p.n;
@@ -392,12 +668,48 @@ hipError_t run_reduction(Problem pr, void *out, int64_t ldo, int add, void *ws, 
 
 int to_status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
 
+int log2_of(int64_t v) {
+    if (v <= 0 || (v & (v - 1))) return -1;
+    int l = 0;
+    while ((int64_t{1} << l) < v) ++l;
+    return l;
+}
+
+Operand dense(const void *p, int64_t ld) {
+    Operand o{};
+    o.p = p;
+    o.ld = ld;
+    return o;
+}
+
+Operand nf4_operand(const ct_nf4_weight *w) {
+    Operand o{};
+    o.p = w->packed;
+    o.ld = w->cols;
+    o.absmax = w->absmax;
+    o.absmax2 = w->absmax2;
+    o.offset = w->offset;
+    o.lb = log2_of(w->blocksize);
+    o.lb2 = w->nested ? log2_of(w->blocksize2) : 0;
+    o.nested = w->nested;
+    return o;
+}
+
+// Conditions of the fused NF4 operand loaders: one first-level block per 32-element unit,
+// 16-byte aligned packed rows, and a storage type whose rounding to bf16 is a single step.
+bool nf4_fusable(const ct_nf4_weight *w) {
+    if (validate_nf4(w) != 0) return false;
+    if (w->storage_dtype != CT_BF16 && w->storage_dtype != CT_F32) return false;
+    if (w->blocksize < 32 || w->cols % 32 != 0) return false;
+    return aligned16(w->packed);
+}
+
 }  // namespace
 }  // namespace ct
 
 using namespace ct;
 
-extern "C" int ct_abi_version(void) { return 1; }
+extern "C" int ct_abi_version(void) { return 2; }
 
 extern "C" const char *ct_status_string(int status) {
     switch (status) {
@@ -407,9 +719,12 @@ extern "C" const char *ct_status_string(int status) {
         case -CT_EINVAL_DTYPE: return "invalid argument: unsupported element type";
         case -CT_EINVAL_BLOCKSIZE: return "invalid argument: unsupported NF4 block size";
         case -CT_EINVAL_WORKSPACE: return "invalid argument: workspace missing or too small";
+        case -CT_EINVAL_LAYOUT: return "invalid argument: NF4 weight layout not supported by the fused path";
         default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
     }
 }
+
+extern "C" int ct_nf4_fused_supported(const ct_nf4_weight *w) { return nf4_fusable(w) ? 1 : 0; }
 
 extern "C" int ct_gemm(const void *a, int64_t lda, int32_t trans_a, const void *b, int64_t ldb, int32_t trans_b,
                        void *c, int64_t ldc, int32_t c_dtype, const void *bias, int32_t beta, int64_t m, int64_t n,
@@ -420,7 +735,9 @@ extern "C" int ct_gemm(const void *a, int64_t lda, int32_t trans_a, const void *
     if (!c || (k > 0 && (!a || !b))) return -CT_EINVAL_POINTER;
     if (ldc < n || lda < (trans_a ? m : k) || ldb < (trans_b ? k : n)) return -CT_EINVAL_SHAPE;
     Problem pr{};
-    pr.p.seg[0] = Segment{static_cast<const uint16_t *>(a), static_cast<const uint16_t *>(b), lda, ldb, k};
+    pr.p.seg[0].a = dense(a, lda);
+    pr.p.seg[0].b = dense(b, ldb);
+    pr.p.seg[0].k = k;
     pr.p.nseg = 1;
     pr.p.m = m;
     pr.p.n = n;
@@ -428,10 +745,11 @@ extern "C" int ct_gemm(const void *a, int64_t lda, int32_t trans_a, const void *
     pr.p.ldc = ldc;
     pr.p.bias = static_cast<const uint16_t *>(bias);
     pr.p.beta = beta;
-    pr.a_src = trans_a ? SRC_KS : SRC_KC;
-    pr.b_src = trans_b ? SRC_KC : SRC_KS;
+    pr.src[0] = trans_a ? SRC_KS : SRC_KC;
+    pr.src[1] = trans_b ? SRC_KC : SRC_KS;
     pr.out = c_dtype;
     pr.splits = 1;
+    pr.tile = -1;
     pr.vec = vec_ok(pr);
     return to_status(run(pr, stream));
 }
@@ -441,18 +759,26 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
                                  int64_t m, int64_t n, int64_t k, int64_t r, hipStream_t stream) {
     if (m < 0 || n < 0 || k < 0 || r < 0) return -CT_EINVAL_SHAPE;
     if (m == 0 || n == 0) return 0;
-    if (w_nf4) return -CT_EINVAL_POINTER;  // the fused NF4 operand is not built into this entry yet
-    if (!x || !w_dense || !out || (r > 0 && (!a || !b || !xa))) return -CT_EINVAL_POINTER;
+    if (!x || !out || (!w_dense == !w_nf4) || (r > 0 && (!a || !b || !xa))) return -CT_EINVAL_POINTER;
     if (ldx < k || ldo < n) return -CT_EINVAL_SHAPE;
-    int st;
+    if (w_nf4) {
+        const int st = validate_nf4(w_nf4);
+        if (st) return st;
+        if (w_nf4->rows != n || w_nf4->cols != k) return -CT_EINVAL_SHAPE;
+        if (!nf4_fusable(w_nf4)) return -CT_EINVAL_LAYOUT;
+    }
     if (r > 0) {
         // xa = x a^T  (NT, bf16 out)
-        st = ct_gemm(x, ldx, 0, a, k, 1, xa, r, CT_BF16, nullptr, 0, m, r, k, stream);
+        const int st = ct_gemm(x, ldx, 0, a, k, 1, xa, r, CT_BF16, nullptr, 0, m, r, k, stream);
         if (st) return st;
     }
     Problem pr{};
-    pr.p.seg[0] = Segment{static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(w_dense), ldx, k, k};
-    pr.p.seg[1] = Segment{static_cast<const uint16_t *>(xa), static_cast<const uint16_t *>(b), r, r, r};
+    pr.p.seg[0].a = dense(x, ldx);
+    pr.p.seg[0].b = w_nf4 ? nf4_operand(w_nf4) : dense(w_dense, k);
+    pr.p.seg[0].k = k;
+    pr.p.seg[1].a = dense(xa, r);
+    pr.p.seg[1].b = dense(b, r);
+    pr.p.seg[1].k = r;
     pr.p.nseg = r > 0 ? 2 : 1;
     pr.p.m = m;
     pr.p.n = n;
@@ -460,10 +786,15 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
     pr.p.ldc = ldo;
     pr.p.bias = static_cast<const uint16_t *>(bias);
     pr.p.beta = 0;
-    pr.a_src = SRC_KC;
-    pr.b_src = SRC_KC;
+    pr.p.code = w_nf4 ? w_nf4->code : nullptr;
+    pr.p.code2 = (w_nf4 && w_nf4->nested) ? w_nf4->code2 : nullptr;
+    pr.src[0] = SRC_KC;
+    pr.src[1] = w_nf4 ? SRC_NF4 : SRC_KC;
+    pr.src[2] = SRC_KC;
+    pr.src[3] = SRC_KC;
     pr.out = CT_BF16;
     pr.splits = 1;
+    pr.tile = -1;
     pr.vec = vec_ok(pr);
     return to_status(run(pr, stream));
 }
@@ -473,28 +804,41 @@ extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_den
                                  int64_t n, int64_t k, int64_t r, int32_t add, hipStream_t stream) {
     if (m < 0 || n < 0 || k < 0 || r < 0) return -CT_EINVAL_SHAPE;
     if (m == 0 || k == 0) return 0;
-    if (w_nf4) return -CT_EINVAL_POINTER;
-    if (!dy || !w_dense || !dx || (r > 0 && (!a || !b || !low))) return -CT_EINVAL_POINTER;
+    if (!dy || !dx || (!w_dense == !w_nf4) || (r > 0 && (!a || !b || !low))) return -CT_EINVAL_POINTER;
     if (lddy < n || lddx < k) return -CT_EINVAL_SHAPE;
-    int st;
+    if (w_nf4) {
+        const int st = validate_nf4(w_nf4);
+        if (st) return st;
+        if (w_nf4->rows != n || w_nf4->cols != k) return -CT_EINVAL_SHAPE;
+        if (!nf4_fusable(w_nf4)) return -CT_EINVAL_LAYOUT;
+    }
     if (r > 0) {
         // low = dy b  (NN, bf16 out)
-        st = ct_gemm(dy, lddy, 0, b, r, 0, low, r, CT_BF16, nullptr, 0, m, r, n, stream);
+        const int st = ct_gemm(dy, lddy, 0, b, r, 0, low, r, CT_BF16, nullptr, 0, m, r, n, stream);
         if (st) return st;
     }
     Problem pr{};
-    pr.p.seg[0] = Segment{static_cast<const uint16_t *>(dy), static_cast<const uint16_t *>(w_dense), lddy, k, n};
-    pr.p.seg[1] = Segment{static_cast<const uint16_t *>(low), static_cast<const uint16_t *>(a), r, k, r};
+    pr.p.seg[0].a = dense(dy, lddy);
+    pr.p.seg[0].b = w_nf4 ? nf4_operand(w_nf4) : dense(w_dense, k);
+    pr.p.seg[0].k = n;
+    pr.p.seg[1].a = dense(low, r);
+    pr.p.seg[1].b = dense(a, k);
+    pr.p.seg[1].k = r;
     pr.p.nseg = r > 0 ? 2 : 1;
     pr.p.m = m;
     pr.p.n = k;
     pr.p.c = dx;
     pr.p.ldc = lddx;
     pr.p.beta = add;
-    pr.a_src = SRC_KC;
-    pr.b_src = SRC_KS;
+    pr.p.code = w_nf4 ? w_nf4->code : nullptr;
+    pr.p.code2 = (w_nf4 && w_nf4->nested) ? w_nf4->code2 : nullptr;
+    pr.src[0] = SRC_KC;
+    pr.src[1] = w_nf4 ? SRC_NF4T : SRC_KS;
+    pr.src[2] = SRC_KC;
+    pr.src[3] = SRC_KS;
     pr.out = CT_BF16;
     pr.splits = 1;
+    pr.tile = -1;
     pr.vec = vec_ok(pr);
     return to_status(run(pr, stream));
 }
@@ -512,13 +856,18 @@ extern "C" int ct_accumulate(float *out, int64_t ldo, const void *left, int64_t 
     if (!out || (j > 0 && (!left || !right))) return -CT_EINVAL_POINTER;
     if (ldo < q || ldl < (trans_l ? p : j) || ldr < (trans_r ? j : q)) return -CT_EINVAL_SHAPE;
     Problem pr{};
-    pr.p.seg[0] = Segment{static_cast<const uint16_t *>(left), static_cast<const uint16_t *>(right), ldl, ldr, j};
+    pr.p.seg[0].a = dense(left, ldl);
+    pr.p.seg[0].b = dense(right, ldr);
+    pr.p.seg[0].k = j;
     pr.p.nseg = 1;
     pr.p.m = p;
     pr.p.n = q;
-    pr.a_src = trans_l ? SRC_KS : SRC_KC;
-    pr.b_src = trans_r ? SRC_KC : SRC_KS;
+    pr.p.c = out;
+    pr.p.ldc = ldo;
+    pr.src[0] = trans_l ? SRC_KS : SRC_KC;
+    pr.src[1] = trans_r ? SRC_KC : SRC_KS;
     pr.out = CT_F32;
+    pr.tile = -1;
     pr.vec = vec_ok(pr);
     int st = 0;
     hipError_t e = run_reduction(pr, out, ldo, add, workspace, workspace_bytes, stream, &st);
@@ -539,7 +888,7 @@ extern "C" int ct_parameter_gradients(const void *x, int64_t ldx, const void *dy
     if (m < 0 || n < 0 || k < 0 || r < 0) return -CT_EINVAL_SHAPE;
     if (r == 0) return 0;
     if (!da || !db) return -CT_EINVAL_POINTER;
-    // da[r, k] = low^T x : L(p=i, j=row) = low[row*r + i]  -> trans_l; R(j=row, q) = x[row*ldx + q]
+    // da[r, k] = low^T x : L(p=i, j=row) = low[row*r + i] -> trans_l; R(j=row, q) = x[row*ldx + q]
     int st = ct_accumulate(da, k, low, r, 1, x, ldx, 0, r, k, m, add, workspace, workspace_bytes, stream);
     if (st) return st;
     // db[n, r] = dy^T xa : L(p=col, j=row) = dy[row*lddy + col] -> trans_l; R(j=row, q) = xa[row*r + q]

@@ -45,6 +45,7 @@ extern "C" {
 #define CT_EINVAL_DTYPE     3  /* unsupported element type                       */
 #define CT_EINVAL_BLOCKSIZE 4  /* unsupported NF4 block size                     */
 #define CT_EINVAL_WORKSPACE 5  /* workspace missing or smaller than required    */
+#define CT_EINVAL_LAYOUT    6  /* NF4 weight layout outside the fused loaders   */
 
 /*
  * Frozen NF4 base weight: the fields of a bitsandbytes QuantState that the reference's
@@ -101,11 +102,24 @@ int ct_gemm(const void *a, int64_t lda, int32_t trans_a,
             int64_t m, int64_t n, int64_t k, hipStream_t stream);
 
 /*
+ * 1 when the fused NF4 operand of ct_forward_linear / ct_input_gradient accepts `w`:
+ * blocksize >= 32, cols % 32 == 0, storage_dtype bf16 or f32 (decoded values reach bf16
+ * in one rounding), packed 16-byte aligned. Otherwise 0: the caller decodes with
+ * ct_nf4_dequant and passes the dense weight (the reference's materialize,
+ * kernels/linear.py:6-13, followed by its dense GEMMs). No counterpart in the reference:
+ * its GEMMs always read a materialised weight.
+ */
+int ct_nf4_fused_supported(const ct_nf4_weight *w);
+
+/*
  * Replaces forward_linear (kernels/linear.py:27-33):
  *   xa  = bf16(x a^T)                               [m, r]   (written)
  *   out = bf16(x w^T + bias + xa b^T)               [m, n]
  * with the base GEMM and the rank-r epilogue as one contraction over k + r columns.
- * Exactly one of w_dense (bf16 [n, k]) or w_nf4 (rows n, cols k) is non-null.
+ * Exactly one of w_dense (bf16 [n, k]) or w_nf4 (rows n, cols k) is non-null. With w_nf4
+ * the weight is decoded tile by tile into LDS inside the GEMM (materialize fused away),
+ * bit-identical to ct_nf4_dequant's bf16 output; returns -CT_EINVAL_LAYOUT when
+ * ct_nf4_fused_supported(w_nf4) is 0.
  * x [m, k] (ldx), a bf16 [r, k], b bf16 [n, r], bias bf16 [n] or null, out [m, n] (ldo),
  * xa bf16 [m, r] contiguous.
  */
@@ -119,8 +133,9 @@ int ct_forward_linear(const void *x, int64_t ldx,
  * Replaces input_gradient (kernels/linear.py:36-39):
  *   low = bf16(dy b)                                 [m, r]   (written)
  *   dx  = bf16(dy w + low a (+ dx if add))           [m, k]
- * dy [m, n] (lddy), w as in ct_forward_linear, a bf16 [r, k], b bf16 [n, r],
- * dx [m, k] (lddx), low bf16 [m, r] contiguous.
+ * dy [m, n] (lddy), w as in ct_forward_linear (an NF4 weight is decoded into LDS in the
+ * transposed layout this product needs), a bf16 [r, k], b bf16 [n, r], dx [m, k] (lddx),
+ * low bf16 [m, r] contiguous.
  */
 int ct_input_gradient(const void *dy, int64_t lddy,
                       const void *w_dense, const ct_nf4_weight *w_nf4,

@@ -43,9 +43,25 @@ def test_library_embeds_gfx950_code_objects():
 
 def test_status_strings_and_version():
     lib = _native.library()
-    assert lib.ct_abi_version() == 1
+    assert lib.ct_abi_version() == 2
     assert lib.ct_status_string(0) == b"success"
     assert b"workspace" in lib.ct_status_string(-5)
+    assert b"fused" in lib.ct_status_string(-6)
+
+
+def test_fused_nf4_operand_conditions():
+    """The fused loaders take blocksize >= 32, cols % 32 == 0, 16-byte aligned packed bytes
+    and a bf16 or f32 storage type; everything else is decoded by ct_nf4_dequant first."""
+    lib = _native.library()
+    desc = _native.NF4Weight(packed=256, absmax=256, code=256, rows=4, cols=64, blocksize=64, nested=0,
+                             storage_dtype=_native.CT_BF16)
+    assert lib.ct_nf4_fused_supported(ctypes.byref(desc)) == 1
+    for field, value in (("cols", 48), ("blocksize", 16), ("storage_dtype", _native.CT_F16), ("packed", 264)):
+        bad = _native.NF4Weight.from_buffer_copy(desc)
+        setattr(bad, field, value)
+        assert lib.ct_nf4_fused_supported(ctypes.byref(bad)) == 0, field
+    desc.storage_dtype = _native.CT_F32
+    assert lib.ct_nf4_fused_supported(ctypes.byref(desc)) == 1
 
 
 def test_host_side_argument_errors_return_negative_status():

@@ -11,7 +11,10 @@ from causal_tuner.kernels import _native
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(256, 384, 320), (37, 80, 96), (1, 1, 1), (129, 65, 17), (64, 8, 4096), (300, 260, 72)]
+# The last two reach the 256x256-tile kernels (>= 256 output tiles); 4100 x 4104 also
+# exercises their ragged edges and, transposed, the scalar (non-16-byte) loaders.
+SHAPES = [(256, 384, 320), (37, 80, 96), (1, 1, 1), (129, 65, 17), (64, 8, 4096), (300, 260, 72),
+          (4096, 4096, 192), (4100, 4104, 136)]
 
 
 def _operand(rows, cols, transposed):
