@@ -351,11 +351,312 @@ struct SegmentRunner {
     }
 };
 
+// ------------------------------------------------------------------ fast segment runner
+// Used when every dense operand is 16-byte aligned with 8-element leading dimensions and
+// every operand spans less than 2 GiB (32-bit buffer offsets). All global reads are raw
+// buffer loads: the hardware range check returns zeros past num_records, and an invalid
+// lane is pointed past the range, so the k-loop body has no branches and the compiler can
+// interleave loads, LDS traffic, NF4 decoding and MFMA within one basic block.
+typedef __attribute__((address_space(3))) void lds_void_t;
+constexpr uint32_t kOOB = 0x80000000u;  // a byte offset beyond every buffer range used here
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int64_t bytes) {
+    const int64_t clamped = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes);
+    // 0x00020000: the raw 32-bit data format word used for gfx9 buffer descriptors.
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)clamped, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+}
+
+template <int SRC, int ROWS, int SWZ_DIV, int THREADS>
+struct Fast;
+
+// Pack elements (half h) of dwords lo and hi into one dword: lo's in the low half.
+__device__ __forceinline__ uint32_t pick16(uint32_t hi, uint32_t lo, int h) {
+    return __builtin_amdgcn_perm(hi, lo, h ? 0x07060302u : 0x05040100u);
+}
+
+// KC: LDS DMA. Each wave instruction moves 64 x 16 bytes = 8 tile rows x 8 chunks; lane l
+// lands in slot base + l (row l/8, physical chunk l%8), so it fetches the global chunk
+// that the swizzle maps to that physical position.
+template <int ROWS, int SWZ_DIV, int THREADS>
+struct Fast<SRC_KC, ROWS, SWZ_DIV, THREADS> {
+    static constexpr int kWaves = THREADS / 64;
+    static constexpr int kInstr = ROWS / (8 * kWaves);
+    static_assert(kInstr >= 1, "tile too small for the workgroup");
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t off[kInstr];  // byte offset of the lane's chunk at k0 = 0
+    int kc[kInstr];        // the lane's first reduction column within the tile
+    int kext;              // reduction extent (< 2^31: fast_ok bounds every operand)
+    int wave;
+    __device__ __forceinline__ void init(const Operand &o, int64_t rows, int64_t kext_, int64_t r0, int tid) {
+        const uint16_t *p = static_cast<const uint16_t *>(o.p) + r0 * o.ld;
+        const int64_t live = rows - r0 < ROWS ? rows - r0 : ROWS;
+        r = make_rsrc(p, live * o.ld * 2);
+        kext = (int)kext_;
+        wave = tid >> 6;
+        const int lane = tid & 63;
+#pragma unroll
+        for (int i = 0; i < kInstr; ++i) {
+            const int row = (wave * kInstr + i) * 8 + (lane >> 3);
+            const int c = (lane & 7) ^ ((row / SWZ_DIV) & 7);
+            kc[i] = c * 8;
+            off[i] = (uint32_t)((row * o.ld + c * 8) * 2);
+        }
+    }
+    __device__ __forceinline__ void issue(uint4 *stage, int64_t k0) {
+#pragma unroll
+        for (int i = 0; i < kInstr; ++i) {
+            const uint32_t o = ((int)k0 + kc[i] < kext) ? off[i] + (uint32_t)(k0 * 2) : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(stage + (wave * kInstr + i) * 64), 16, o, 0,
+                                                     0, 0);
+        }
+    }
+    __device__ __forceinline__ void commit(uint4 *, const float *, const float *, float) const {}
+};
+
+// Store R bf16 values (R/2 dwords) at byte offset `byte` of the stage.
+template <int R>
+__device__ __forceinline__ void store_part(uint4 *stage, int byte, const uint32_t (&w)[R / 2]) {
+    char *b = reinterpret_cast<char *>(stage) + byte;
+    if constexpr (R == 8) *reinterpret_cast<uint4 *>(b) = make_uint4(w[0], w[1], w[2], w[3]);
+    else if constexpr (R == 4) *reinterpret_cast<uint2 *>(b) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint32_t *>(b) = w[0];
+}
+
+// KS: 8x8 blocks (8 reduction rows x 8 output rows), split over LPB lanes that take
+// R = 8 / LPB reduction rows each; transposed in registers, R values per LDS write.
+template <int ROWS, int SWZ_DIV, int THREADS>
+struct Fast<SRC_KS, ROWS, SWZ_DIV, THREADS> {
+    static constexpr int kLPB = THREADS / ROWS;
+    static constexpr int R = 8 / kLPB;
+    static_assert(kLPB >= 1 && kLPB <= 4, "unsupported tile / workgroup ratio");
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t off0, pitch;
+    int col, chunk, h;
+    bool valid;
+    uint4 v[R];
+    __device__ __forceinline__ void init(const Operand &o, int64_t rows, int64_t kext, int64_t r0, int tid) {
+        const int b = tid % ROWS;
+        h = tid / ROWS;
+        col = (b % (ROWS / 8)) * 8;
+        chunk = b / (ROWS / 8);
+        const uint16_t *p = static_cast<const uint16_t *>(o.p) + r0;
+        r = make_rsrc(p, kext > 0 ? ((kext - 1) * o.ld + (rows - r0)) * 2 : 0);
+        valid = r0 + col < rows;
+        pitch = (uint32_t)(o.ld * 2);
+        off0 = (uint32_t)(((chunk * 8 + h * R) * o.ld + col) * 2);
+    }
+    __device__ __forceinline__ void issue(uint4 *, int64_t k0) {
+        const uint32_t base = off0 + (uint32_t)(k0 * pitch);
+#pragma unroll
+        for (int i = 0; i < R; ++i) v[i] = buf_load16(r, valid ? base + i * pitch : kOOB);
+    }
+    __device__ __forceinline__ void commit(uint4 *stage, const float *, const float *, float) const {
+        const uint32_t *d = reinterpret_cast<const uint32_t *>(v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t w[R / 2];
+#pragma unroll
+            for (int q = 0; q < R / 2; ++q) w[q] = pick16(d[(2 * q + 1) * 4 + (j >> 1)], d[(2 * q) * 4 + (j >> 1)], j & 1);
+            store_part<R>(stage, slot<SWZ_DIV>(col + j, chunk) * 16 + h * R * 2, w);
+        }
+    }
+};
+
+// NF4 (nested), reduction along the weight's columns: units of 32 elements of one row.
+template <int ROWS, int SWZ_DIV, int THREADS>
+struct Fast<SRC_NF4, ROWS, SWZ_DIV, THREADS> {
+    static constexpr int kUnits = ROWS * 2;
+    static constexpr int kPer = (kUnits + THREADS - 1) / THREADS;
+    __amdgpu_buffer_rsrc_t rq, ra, r2;
+    uint32_t e0[kPer];  // element index of the unit at k0 = 0 (whole weight)
+    int row[kPer], half[kPer];
+    int kext;
+    int lb, lb2;
+    uint4 q[kPer];
+    uint32_t qa[kPer];
+    float a2[kPer];
+    bool ok[kPer];
+    __device__ __forceinline__ void init(const Operand &o, int64_t rows, int64_t kext_, int64_t r0, int tid) {
+        kext = (int)kext_;
+        lb = o.lb;
+        lb2 = o.lb2;
+        const int64_t n = rows * o.ld;
+        rq = make_rsrc(o.p, (n + 1) / 2);
+        const int64_t nb = (n + (int64_t{1} << lb) - 1) >> lb;
+        ra = make_rsrc(o.absmax, nb);
+        r2 = make_rsrc(o.absmax2, ((nb + (int64_t{1} << lb2) - 1) >> lb2) * 4);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int u = (tid + i * THREADS) % kUnits;
+            row[i] = u >> 1;
+            half[i] = u & 1;
+            const int64_t gr = r0 + row[i];
+            e0[i] = gr < rows ? (uint32_t)(gr * o.ld + half[i] * 32) : 0xffffffffu;
+        }
+    }
+    __device__ __forceinline__ void issue(uint4 *, int64_t k0) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            ok[i] = e0[i] != 0xffffffffu && (int)k0 + half[i] * 32 < kext;
+            const uint32_t e = e0[i] + (uint32_t)k0;
+            const uint32_t g = e >> lb;
+            q[i] = buf_load16(rq, ok[i] ? e >> 1 : kOOB);
+            qa[i] = buf_load1(ra, ok[i] ? g : kOOB);
+            a2[i] = __builtin_bit_cast(float, buf_load4(r2, ok[i] ? (g >> lb2) * 4 : kOOB));
+        }
+    }
+    __device__ __forceinline__ void commit(uint4 *stage, const float *lcode, const float *lcode2,
+                                           float offset) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const float s = ok[i] ? lcode2[qa[i] & 255u] * a2[i] + offset : 0.f;
+            const int c0 = half[i] * 4;
+            stage[slot<SWZ_DIV>(row[i], c0 + 0)] = nf4_decode8(q[i].x, s, lcode);
+            stage[slot<SWZ_DIV>(row[i], c0 + 1)] = nf4_decode8(q[i].y, s, lcode);
+            stage[slot<SWZ_DIV>(row[i], c0 + 2)] = nf4_decode8(q[i].z, s, lcode);
+            stage[slot<SWZ_DIV>(row[i], c0 + 3)] = nf4_decode8(q[i].w, s, lcode);
+        }
+    }
+};
+
+// NF4 (nested), reduction along the weight's rows: units of 8 weight rows x 8 columns,
+// split over LPB lanes that take R = 8 / LPB weight rows each.
+template <int ROWS, int SWZ_DIV, int THREADS>
+struct Fast<SRC_NF4T, ROWS, SWZ_DIV, THREADS> {
+    static constexpr int kCB = ROWS / 8;
+    static constexpr int kLPB = THREADS / ROWS;
+    static constexpr int R = 8 / kLPB;
+    static_assert(kLPB >= 1 && kLPB <= 4, "unsupported tile / workgroup ratio");
+    __amdgpu_buffer_rsrc_t rq, ra, r2;
+    uint32_t e0;  // element index of (weight row chunk*8 + h*R, column r0 + col) at k0 = 0
+    uint32_t ld;
+    int col, chunk, h, row0;
+    bool colok;
+    int kext;
+    int lb, lb2;
+    uint32_t d[R], qa[R];
+    float a2[R];
+    bool ok[R];
+    __device__ __forceinline__ void init(const Operand &o, int64_t rows, int64_t kext_, int64_t r0, int tid) {
+        kext = (int)kext_;
+        lb = o.lb;
+        lb2 = o.lb2;
+        const int64_t n = kext_ * o.ld;  // weight rows x weight columns
+        rq = make_rsrc(o.p, (n + 1) / 2);
+        const int64_t nb = (n + (int64_t{1} << lb) - 1) >> lb;
+        ra = make_rsrc(o.absmax, nb);
+        r2 = make_rsrc(o.absmax2, ((nb + (int64_t{1} << lb2) - 1) >> lb2) * 4);
+        const int b = tid % ROWS;
+        h = tid / ROWS;
+        col = (b % kCB) * 8;
+        chunk = b / kCB;
+        row0 = chunk * 8 + h * R;
+        colok = r0 + col < rows;
+        ld = (uint32_t)o.ld;
+        e0 = (uint32_t)(row0 * o.ld + r0 + col);
+    }
+    __device__ __forceinline__ void issue(uint4 *, int64_t k0) {
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            ok[i] = colok && (int)k0 + row0 + i < kext;
+            const uint32_t e = e0 + (uint32_t)(k0 + i) * ld;
+            const uint32_t g = e >> lb;
+            d[i] = buf_load4(rq, ok[i] ? e >> 1 : kOOB);
+            qa[i] = buf_load1(ra, ok[i] ? g : kOOB);
+            a2[i] = __builtin_bit_cast(float, buf_load4(r2, ok[i] ? (g >> lb2) * 4 : kOOB));
+        }
+    }
+    __device__ __forceinline__ void commit(uint4 *stage, const float *lcode, const float *lcode2,
+                                           float offset) const {
+        float s[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) s[i] = ok[i] ? lcode2[qa[i] & 255u] * a2[i] + offset : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int shift = (j & 1) ? 8 * (j >> 1) : 8 * (j >> 1) + 4;
+            uint32_t w[R / 2];
+#pragma unroll
+            for (int q = 0; q < R / 2; ++q)
+                w[q] = pack_bf16x2(lcode[(d[2 * q] >> shift) & 15u] * s[2 * q],
+                                   lcode[(d[2 * q + 1] >> shift) & 15u] * s[2 * q + 1]);
+            store_part<R>(stage, slot<SWZ_DIV>(col + j, chunk) * 16 + h * R * 2, w);
+        }
+    }
+};
+
+template <int BM, int BN, int SA, int SB, int WAVES_M, int WAVES_N>
+struct FastRunner {
+    static constexpr int THREADS = 64 * WAVES_M * WAVES_N;
+    static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+    static constexpr int FM = WM / 16, FN = WN / 16;
+    static constexpr int kStage = (BM + BN) * 8;
+
+    __device__ __forceinline__ static void run(const Segment &sg, int64_t m, int64_t n, int64_t m0, int64_t n0,
+                                               int64_t tbeg, int64_t tend, f32x4 (&acc)[FM][FN], uint4 *lds,
+                                               const float *lcode, const float *lcode2, int tid, int wm0,
+                                               int wn0) {
+        if (tbeg >= tend) return;
+        const int lane = tid & 63;
+        Fast<SA, BM, 1, THREADS> la;
+        Fast<SB, BN, FN, THREADS> lb;
+        la.init(sg.a, m, sg.k, m0, tid);
+        lb.init(sg.b, n, sg.k, n0, tid);
+        const float off_a = is_nf4<SA>() ? *sg.a.offset : 0.f;
+        const float off_b = is_nf4<SB>() ? *sg.b.offset : 0.f;
+        __syncthreads();  // every wave is done with the buffers of a previous segment
+        la.issue(lds, tbeg * kBK);
+        lb.issue(lds + BM * 8, tbeg * kBK);
+        la.commit(lds, lcode, lcode2, off_a);
+        lb.commit(lds + BM * 8, lcode, lcode2, off_b);
+        __builtin_amdgcn_s_waitcnt(0);  // LDS-DMA writes complete before the barrier publishes them
+        __syncthreads();
+        for (int64_t t = tbeg; t < tend; ++t) {
+            uint4 *cur = lds + ((t - tbeg) & 1) * kStage;
+            uint4 *nxt = lds + (((t - tbeg) & 1) ^ 1) * kStage;
+            // Tile t+1 (past the end: masked to zeros, never consumed) into the other stage,
+            // which every wave finished reading before the previous barrier.
+            la.issue(nxt, (t + 1) * kBK);
+            lb.issue(nxt + BM * 8, (t + 1) * kBK);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int ks = 0; ks < kBK / 32; ++ks) {
+                const int chunk = ks * 4 + (lane >> 4);
+                uint4 af[FM], bf[FN];
+#pragma unroll
+                for (int i = 0; i < FM; ++i) af[i] = cur[slot<1>(wm0 + i * 16 + (lane & 15), chunk)];
+#pragma unroll
+                for (int j = 0; j < FN; ++j) bf[j] = cur[BM * 8 + slot<FN>(wn0 + (lane & 15) * FN + j, chunk)];
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            la.commit(nxt, lcode, lcode2, off_a);
+            lb.commit(nxt + BM * 8, lcode, lcode2, off_b);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
+    }
+};
+
 // ------------------------------------------------------------------------- the kernel body
-template <int BM, int BN, int A0, int B0, int A1, int B1, bool VEC, int OUT>
+template <int BM, int BN, int A0, int B0, int A1, int B1, int MODE, int OUT, int WAVES_M = 2, int WAVES_N = 2>
 __device__ __forceinline__ void gemm_body(const GemmParams &p) {
-    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr bool VEC = MODE != 0;
+    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int FM = WM / 16, FN = WN / 16;
+    static_assert(MODE == 2 || (WAVES_M == 2 && WAVES_N == 2), "the generic runner uses 4 waves");
     constexpr bool kNF4 = is_nf4<A0>() || is_nf4<B0>() || is_nf4<A1>() || is_nf4<B1>();
     __shared__ uint4 lds[2 * (BM + BN) * 8];
     __shared__ float lcode[kNF4 ? 16 : 1];
@@ -363,7 +664,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm0 = (wave & 1) * WM, wn0 = (wave >> 1) * WN;
+    const int wm0 = (wave % WAVES_M) * WM, wn0 = (wave / WAVES_M) * WN;
 
     // Tile order: contiguous ranges per XCD, M-grouped inside a range.
     const int tiles = p.tiles_m * p.tiles_n;
@@ -381,7 +682,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 
     if constexpr (kNF4) {
         if (tid < 16) lcode[tid] = p.code[tid];
-        if (p.code2) lcode2[tid] = p.code2[tid];
+        if (p.code2 && tid < 256) lcode2[tid] = p.code2[tid];
         // made visible by the barrier that precedes the first tile store
     }
 
@@ -397,13 +698,21 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     const int64_t tend = tbeg + p.tiles_per_split < t0 + t1 ? tbeg + p.tiles_per_split : t0 + t1;
     {
         const int64_t b = tbeg, e = tend < t0 ? tend : t0;
-        SegmentRunner<BM, BN, A0, B0, VEC>::run(p.seg[0], p.m, p.n, m0, n0, b, e, acc, lds, lcode, lcode2, tid,
-                                                wm0, wn0);
+        if constexpr (MODE == 2)
+            FastRunner<BM, BN, A0, B0, WAVES_M, WAVES_N>::run(p.seg[0], p.m, p.n, m0, n0, b, e, acc, lds, lcode, lcode2, tid, wm0,
+                                            wn0);
+        else
+            SegmentRunner<BM, BN, A0, B0, VEC>::run(p.seg[0], p.m, p.n, m0, n0, b, e, acc, lds, lcode, lcode2,
+                                                    tid, wm0, wn0);
     }
     if (t1 > 0) {
         const int64_t b = tbeg > t0 ? tbeg - t0 : 0, e = tend - t0;
-        SegmentRunner<BM, BN, A1, B1, VEC>::run(p.seg[1], p.m, p.n, m0, n0, b, e, acc, lds, lcode, lcode2, tid,
-                                                wm0, wn0);
+        if constexpr (MODE == 2)
+            FastRunner<BM, BN, A1, B1, WAVES_M, WAVES_N>::run(p.seg[1], p.m, p.n, m0, n0, b, e, acc, lds, lcode, lcode2, tid, wm0,
+                                            wn0);
+        else
+            SegmentRunner<BM, BN, A1, B1, VEC>::run(p.seg[1], p.m, p.n, m0, n0, b, e, acc, lds, lcode, lcode2,
+                                                    tid, wm0, wn0);
     }
 
     // ------------------------------------------------------------------ epilogue
@@ -465,15 +774,23 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 }
 
 // 256x256 tiles: one workgroup per CU, 512 registers per lane (accumulators in AGPRs).
-template <int A0, int B0, int A1, int B1, bool VEC, int OUT>
+template <int A0, int B0, int A1, int B1, int MODE, int OUT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_big(
     const GemmParams p) {
-    gemm_body<256, 256, A0, B0, A1, B1, VEC, OUT>(p);
+    gemm_body<256, 256, A0, B0, A1, B1, MODE, OUT>(p);
 }
 
-template <int BM, int BN, int A0, int B0, int A1, int B1, bool VEC, int OUT>
+template <int BM, int BN, int A0, int B0, int A1, int B1, int MODE, int OUT>
 __global__ __launch_bounds__(kThreads) void gemm_small(const GemmParams p) {
-    gemm_body<BM, BN, A0, B0, A1, B1, VEC, OUT>(p);
+    gemm_body<BM, BN, A0, B0, A1, B1, MODE, OUT>(p);
+}
+
+// 256x256 tiles, 8 waves (two per SIMD) of 64x128: each wave's accumulators fit in 128
+// registers, and the second wave on a SIMD issues MFMA while the first waits on LDS or
+// the barrier. Fast operand path only.
+template <int A0, int B0, int A1, int B1, int OUT>
+__global__ __launch_bounds__(512) void gemm_big8(const GemmParams p) {
+    gemm_body<256, 256, A0, B0, A1, B1, 2, OUT, 4, 2>(p);
 }
 
 // Deterministic reduction of fp32 split partials: out = sum_z ws[z] (+ out), in z order.
@@ -508,6 +825,11 @@ struct Problem {
     int tile;     // forced tile, or -1 to choose
 };
 
+// Byte extent of a dense operand whose output-dimension extent is `rows`.
+int64_t dense_extent(const Operand &o, int src, int64_t rows, int64_t k) {
+    return src == SRC_KS ? ((k > 0 ? k - 1 : 0) * o.ld + rows) * 2 : rows * o.ld * 2;
+}
+
 bool aligned16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
 constexpr bool is_nf4_host(int src) { return src == SRC_NF4 || src == SRC_NF4T; }
 
@@ -528,6 +850,28 @@ bool vec_ok(const Problem &pr) {
     return true;
 }
 
+// The fast runner: 16-byte operand access (vec_ok), 32-bit buffer offsets, nested NF4.
+bool fast_ok(const Problem &pr) {
+    if (!pr.vec) return false;
+    const GemmParams &p = pr.p;
+    constexpr int64_t kLimit = int64_t{1} << 31;
+    for (int s = 0; s < p.nseg; ++s) {
+        const Segment &g = p.seg[s];
+        const int src[2] = {pr.src[2 * s], pr.src[2 * s + 1]};
+        const Operand *op[2] = {&g.a, &g.b};
+        const int64_t rows[2] = {p.m, p.n};
+        for (int i = 0; i < 2; ++i) {
+            if (is_nf4_host(src[i])) {
+                const int64_t n = (src[i] == SRC_NF4 ? rows[i] : g.k) * op[i]->ld;
+                if (!op[i]->nested || n >= kLimit) return false;
+            } else if (dense_extent(*op[i], src[i], rows[i], g.k) >= kLimit) {
+                return false;
+            }
+        }
+    }
+    return true;
+}
+
 // Largest tile that still yields about one workgroup per CU (256 CUs).
 int choose_tile(int64_t m, int64_t n, int splits) {
     for (int t = TILE_256; t < TILE_64; ++t) {
@@ -537,27 +881,31 @@ int choose_tile(int64_t m, int64_t n, int splits) {
     return TILE_64;
 }
 
-template <int A0, int B0, int A1, int B1, bool VEC, int OUT>
+template <int A0, int B0, int A1, int B1, int MODE, int OUT>
 hipError_t launch_cfg(const GemmParams &p0, int tile, int splits, hipStream_t s) {
     GemmParams p = p0;
     const int e = kTileEdge[tile];
     p.tiles_m = (int)cdiv(p.m, e);
     p.tiles_n = (int)cdiv(p.n, e);
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)splits);
-    if (tile == TILE_256) gemm_big<A0, B0, A1, B1, VEC, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
-    else if (tile == TILE_128) gemm_small<128, 128, A0, B0, A1, B1, VEC, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
-    else gemm_small<64, 64, A0, B0, A1, B1, VEC, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
+    if (tile == TILE_256 && MODE == 2) gemm_big8<A0, B0, A1, B1, OUT><<<grid, dim3(512), 0, s>>>(p);
+    else if (tile == TILE_256) gemm_big<A0, B0, A1, B1, MODE, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
+    else if (tile == TILE_128) gemm_small<128, 128, A0, B0, A1, B1, MODE, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
+    else gemm_small<64, 64, A0, B0, A1, B1, MODE, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
     return hipGetLastError();
+}
+
+template <int A0, int B0, int A1, int B1, int OUT>
+hipError_t launch_mode(const Problem &pr, int tile, hipStream_t s) {
+    if (fast_ok(pr)) return launch_cfg<A0, B0, A1, B1, 2, OUT>(pr.p, tile, pr.splits, s);
+    if (pr.vec) return launch_cfg<A0, B0, A1, B1, 1, OUT>(pr.p, tile, pr.splits, s);
+    return launch_cfg<A0, B0, A1, B1, 0, OUT>(pr.p, tile, pr.splits, s);
 }
 
 template <int A0, int B0, int A1, int B1>
 hipError_t launch_vec_out(const Problem &pr, int tile, hipStream_t s) {
-    if (pr.vec) {
-        return pr.out == CT_F32 ? launch_cfg<A0, B0, A1, B1, true, CT_F32>(pr.p, tile, pr.splits, s)
-                                : launch_cfg<A0, B0, A1, B1, true, CT_BF16>(pr.p, tile, pr.splits, s);
-    }
-    return pr.out == CT_F32 ? launch_cfg<A0, B0, A1, B1, false, CT_F32>(pr.p, tile, pr.splits, s)
-                            : launch_cfg<A0, B0, A1, B1, false, CT_BF16>(pr.p, tile, pr.splits, s);
+    return pr.out == CT_F32 ? launch_mode<A0, B0, A1, B1, CT_F32>(pr, tile, s)
+                            : launch_mode<A0, B0, A1, B1, CT_BF16>(pr, tile, s);
 }
 
 int64_t total_tiles(const GemmParams &p) {
@@ -591,11 +939,9 @@ hipError_t run(Problem &pr, hipStream_t s) {
         // NF4 loaders keep their own alignment (checked by nf4_fusable); VEC covers the
         // dense operands and the output.
         case CT_LAYOUT(SRC_KC, SRC_NF4, SRC_KC, SRC_KC):
-            return pr.vec ? launch_cfg<SRC_KC, SRC_NF4, SRC_KC, SRC_KC, true, CT_BF16>(p, tile, pr.splits, s)
-                          : launch_cfg<SRC_KC, SRC_NF4, SRC_KC, SRC_KC, false, CT_BF16>(p, tile, pr.splits, s);
+            return launch_mode<SRC_KC, SRC_NF4, SRC_KC, SRC_KC, CT_BF16>(pr, tile, s);
         case CT_LAYOUT(SRC_KC, SRC_NF4T, SRC_KC, SRC_KS):
-            return pr.vec ? launch_cfg<SRC_KC, SRC_NF4T, SRC_KC, SRC_KS, true, CT_BF16>(p, tile, pr.splits, s)
-                          : launch_cfg<SRC_KC, SRC_NF4T, SRC_KC, SRC_KS, false, CT_BF16>(p, tile, pr.splits, s);
+            return launch_mode<SRC_KC, SRC_NF4T, SRC_KC, SRC_KS, CT_BF16>(pr, tile, s);
         default:
             return hipErrorInvalidValue;
     }
