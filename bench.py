@@ -8,17 +8,22 @@ project_group((q, k, v), x), project_group((o,), y), project_group((gate, up), x
 project_group((down,), h), then autograd backward with ~N(0, 1) upstream gradients
 (input gradients and fp32 dA/dB for all seven). Synthetic data, random-init weights.
 
-value  = algorithmic TFLOP/s of the step, 2M[2KN + 3r(K+N)] summed over the seven
-         projections (6.449 TFLOP; the reference's xa recompute is not counted).
-Also reported on the same line: the dominant kernel's roofline (HIP-event timed), the
-standalone NF4 dequant of C2 (GB/s vs 8 TB/s), a hipBLASLt bf16 GEMM probe, and the
-reference op sequence timed on the host CPU (cpu_baseline).
+value     algorithmic TFLOP/s of the step, 2M[2KN + 3r(K+N)] summed over the seven
+          projections (6.449 TFLOP; the reference's xa recompute is not counted).
+roofline  the dominant kernel family, timed with HIP events around each of its launches
+          inside the timed region (ct_profile_*), against the 2.5 PFLOP/s bf16 dense peak;
+          traffic from profiles/<family>_traffic.json (rocprofv3 --pmc, see --pmc-summary).
+kernels   the same per-family breakdown for every timed family.
+dequant   C2: standalone NF4 dequant, GB/s against the 8 TB/s HBM peak.
+cpu_baseline  the reference's op sequence on the host CPU (oracle/lora.py), bounded sample.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-dequant]
+    python bench.py --copy-probe MiB ...     # first run a plain copy of that size (PMC scale)
+    python bench.py --pmc-summary FETCH.csv WRITE.csv FAMILY MiB   # write profiles/FAMILY_traffic.json
 """
 
 import argparse
-import ctypes
+import csv
 import json
 import os
 import sys
@@ -97,31 +102,6 @@ def time_events(fn, iters, warmup=3):
     return start.elapsed_time(stop) / iters
 
 
-def dominant_kernel_roofline(device):
-    """The base NT GEMM of the largest projection (gate: 8192 x 4096 -> 11008), the
-    instantiation that carries most of the step's MFMA work, timed alone with HIP events."""
-    from causal_tuner.kernels import _native
-    lib = _native.library()
-    x = torch.randn(T, D, device=device).to(torch.bfloat16)
-    w = (torch.randn(I, D, device=device) * 0.02).to(torch.bfloat16)
-    out = torch.empty(T, I, device=device, dtype=torch.bfloat16)
-    stream = _native.stream_of(x)
-
-    def run():
-        status = lib.ct_gemm(x.data_ptr(), D, 0, w.data_ptr(), D, 1, out.data_ptr(), I, _native.CT_BF16, None, 0,
-                             T, I, D, stream)
-        assert status == 0
-    ms = time_events(run, 20)
-    flops = 2.0 * T * I * D
-    achieved = flops / (ms * 1e-3) / 1e12
-    ms_torch = time_events(lambda: torch.mm(x, w.T, out=out), 20)
-    return {"kernel": "gemm_kernel<128,128,2,KC,KC,vec,bf16> (ct_gemm NT: 8192x4096 . 4096x11008)",
-            "bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None, "avg_ms": round(ms, 4),
-            "flops_per_launch": flops,
-            "hipblaslt_probe_tflops": round(flops / (ms_torch * 1e-3) / 1e12, 2)}
-
-
 def dequant_measure(device):
     """C2: standalone NF4 dequant of [28672, 8192] (and [8192, 8192]) to bf16, HBM GB/s."""
     from causal_tuner.kernels.nf4_cuda import dequantize_nf4_into
@@ -186,21 +166,97 @@ def cpu_baseline(budget_s=12.0):
                       f"fwd+bwd at {tokens} of {T} tokens, {reps} reps in {elapsed:.1f} s"}
 
 
+FAMILIES = {
+    "fwd_gemm": ("CT_PROF_FWD_GEMM", "fused projection GEMM of ct_forward_linear (x w^T + xa b^T, NF4 decoded in LDS)"),
+    "dx_gemm": ("CT_PROF_DX_GEMM", "fused projection GEMM of ct_input_gradient (dy w + low a, NF4 decoded in LDS)"),
+    "param": ("CT_PROF_PARAM", "ct_parameter_gradients (dA = low^T x, dB = dy^T xa, fp32)"),
+    "lowrank": ("CT_PROF_LOWRANK", "rank-r products inside the entry points (xa = x a^T, low = dy b)"),
+}
+# The dx family is one kernel instantiation for every C3 projection (all reach 256x256 tiles).
+KERNEL_NAMES = {"dx_gemm": "gemm_big8<KC, NF4T, KC, KS>", "fwd_gemm": "gemm_big8<KC, NF4, KC, KC> (q,o,gate,up,down) "
+                "+ gemm_small<64,64,...> (k, v)"}
+
+
+def traffic_from_profiles(kernel_key):
+    """HBM bytes per launch of the dominant kernel, measured by rocprofv3 --pmc (FETCH_SIZE,
+    WRITE_SIZE) and scaled against a copy kernel of known size; see profiles/."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_key}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def copy_probe(mib):
+    """A plain device-to-device copy of `mib` MiB: torch's copy kernel reads and writes
+    exactly that many bytes, which scales the FETCH_SIZE / WRITE_SIZE counters."""
+    src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def pmc_summary(fetch_csv, write_csv, family, mib):
+    """Per-launch HBM traffic of a kernel family from two rocprofv3 --pmc runs (FETCH_SIZE,
+    WRITE_SIZE, KiB per dispatch), each scaled by the same counter's reading for the copy
+    probe of `mib` MiB; written to profiles/<family>_traffic.json."""
+    patterns = {"dx_gemm": "gemm_big8<0, 3, 0, 1, 2>", "fwd_gemm": "gemm_big8<0, 2, 0, 0, 2>"}
+    copy_bytes = mib << 20
+
+    def read(path, counter):
+        rows = list(csv.DictReader(open(path)))
+        kernel, copy = [], []
+        for r in rows:
+            if r.get("Counter_Name") != counter:
+                continue
+            name, value = r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0
+            if patterns[family] in name:
+                kernel.append(value)
+            elif "copy" in name.lower() and value > 0.5 * copy_bytes:
+                copy.append(value)
+        return sum(kernel) / max(len(kernel), 1), len(kernel), max(copy) if copy else None
+
+    fetch, n_fetch, copy_fetch = read(fetch_csv, "FETCH_SIZE")
+    write, n_write, copy_write = read(write_csv, "WRITE_SIZE")
+    scale_f = copy_bytes / copy_fetch if copy_fetch else 1.0
+    scale_w = copy_bytes / copy_write if copy_write else 1.0
+    out = {"family": family, "kernel": patterns[family], "dispatches": [n_fetch, n_write],
+           "fetch_bytes_raw": fetch, "write_bytes_raw": write,
+           "copy_probe_bytes": copy_bytes, "copy_fetch_raw": copy_fetch, "copy_write_raw": copy_write,
+           "fetch_scale": scale_f, "write_scale": scale_w,
+           "bytes_per_launch": fetch * scale_f + write * scale_w}
+    path = os.path.join(ROOT, "profiles", f"{family}_traffic.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--pmc-summary":
+        pmc_summary(sys.argv[2], sys.argv[3], sys.argv[4], int(sys.argv[5]))
+        return
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=10)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    parser.add_argument("--no-dequant", action="store_true", help="skip the standalone dequant leg")
+    parser.add_argument("--copy-probe", type=int, default=0, metavar="MiB",
+                        help="first run a plain device copy of this size (scales PMC byte counters)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        print("bench.py measures one GPU: every GPU box here has one, and this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs the MI355X (no HIP device visible)", file=sys.stderr)
         sys.exit(2)
+    from causal_tuner.kernels import _native
     device = "cuda"
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
 
     log("building C3 layer (NF4 quantization of seven projections)...")
     modules, inputs, grads = build_layer(device)
@@ -208,20 +264,39 @@ def main():
         layer_step(modules, inputs, grads)
     torch.cuda.synchronize()
     log(f"warmup done; timing {args.steps} steps")
-    start = time.perf_counter()
-    for _ in range(args.steps):
-        layer_step(modules, inputs, grads)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - start
+    mask = sum(getattr(_native, name) for name, _ in FAMILIES.values())
+    with _native.KernelTimer(mask, capacity=64 * max(args.steps, 1)) as timer:
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(args.steps):
+            layer_step(modules, inputs, grads)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - start
+        families = {}
+        for key, (name, what) in FAMILIES.items():
+            ms, launches, work = timer.read(getattr(_native, name))
+            families[key] = {"what": what, "launches": launches, "total_ms": round(ms, 4),
+                             "avg_us": round(ms * 1e3 / max(launches, 1), 2),
+                             "tflops": round(work / (ms * 1e-3) / 1e12, 2) if ms else None,
+                             "share_of_step": round(ms / (elapsed * 1e3), 4)}
     ms_per_step = elapsed * 1e3 / args.steps
     tflops = step_flops() / (ms_per_step * 1e-3) / 1e12
     log(f"C3 step: {ms_per_step:.3f} ms, {tflops:.1f} TFLOP/s")
+    for key, v in families.items():
+        log(f"  {key:9s} {v['launches']:4d} launches  avg {v['avg_us']:9.1f} us  {v['tflops']} TFLOP/s  "
+            f"{100 * v['share_of_step']:.1f}% of step")
+    dominant = max(("fwd_gemm", "dx_gemm"), key=lambda k: families[k]["total_ms"])
+    d = families[dominant]
+    achieved = d["tflops"]
+    roofline = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic_from_profiles(dominant),
+                "kernel": KERNEL_NAMES.get(dominant, dominant), "family": dominant, "avg_us": d["avg_us"],
+                "launches": d["launches"],
+                "flops_per_launch": "2 M N (K + r) forward, 2 M K (N + r) dx, per projection"}
     del modules, inputs, grads
     torch.cuda.empty_cache()
 
-    roofline = dominant_kernel_roofline(device)
-    log(f"dominant kernel: {roofline}")
-    dequant = dequant_measure(device)
+    dequant = None if args.no_dequant else dequant_measure(device)
     log(f"dequant: {dequant}")
     cpu = None if args.no_cpu else cpu_baseline()
     log(f"cpu baseline: {cpu}")
@@ -238,6 +313,7 @@ def main():
                    "flops_per_step": step_flops()},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "kernels": families,
         "dequant": {"workload": "C2: standalone NF4 dequant to bf16", "bound": "hbm", "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "results": dequant},
     }

@@ -15,6 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIBRARY = os.path.normpath(os.path.join(_HERE, "..", "..", "lib", "libcausal_tuner_hip.so"))
 
 CT_F32, CT_F16, CT_BF16 = 0, 1, 2
+CT_PROF_FWD_GEMM, CT_PROF_DX_GEMM, CT_PROF_DEQUANT, CT_PROF_PARAM, CT_PROF_LOWRANK = 1, 2, 4, 8, 16
 DTYPE_CODES = {torch.float32: CT_F32, torch.float16: CT_F16, torch.bfloat16: CT_BF16}
 
 _P = ctypes.c_void_p
@@ -46,6 +47,10 @@ _SIGNATURES = {
     "ct_parameter_gradients": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32,
                                               _P, _I64, _P]),
     "ct_accumulate_workspace": (_I64, [_I64, _I64, _I64]),
+    "ct_profile_begin": (ctypes.c_int, [_I32, _I32]),
+    "ct_profile_read": (ctypes.c_int, [_I32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64),
+                                       ctypes.POINTER(ctypes.c_double)]),
+    "ct_profile_end": (ctypes.c_int, []),
     "ct_accumulate": (ctypes.c_int, [_P, _I64, _P, _I64, _I32, _P, _I64, _I32, _I64, _I64, _I64, _I32, _P, _I64,
                                      _P]),
 }
@@ -112,3 +117,27 @@ def nf4_descriptor(weight, state):
         offset=state.offset.data_ptr() if nested else None, rows=rows, cols=cols, blocksize=int(state.blocksize),
         blocksize2=int(aux.blocksize) if nested else 0, nested=int(nested), storage_dtype=dtype_code(state.dtype))
     return desc
+
+
+class KernelTimer:
+    """Time the launches of some kernel families with HIP events (ct_profile_*).
+
+    Used by the benchmark inside its timed region: `read(family)` returns
+    (total_ms, launches, algorithmic_work) for the launches made while active."""
+
+    def __init__(self, families, capacity=4096):
+        self.families, self.capacity = families, capacity
+
+    def __enter__(self):
+        check(library().ct_profile_begin(self.families, self.capacity), "ct_profile_begin")
+        return self
+
+    def read(self, family):
+        ms, n, work = ctypes.c_double(), _I64(), ctypes.c_double()
+        check(library().ct_profile_read(family, ctypes.byref(ms), ctypes.byref(n), ctypes.byref(work)),
+              "ct_profile_read")
+        return ms.value, n.value, work.value
+
+    def __exit__(self, *exc):
+        library().ct_profile_end()
+        return False

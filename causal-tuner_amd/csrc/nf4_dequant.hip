@@ -14,6 +14,7 @@
 // is an LDS read whose 16 (resp. 256) fp32 entries occupy distinct banks.
 
 #include "common.hpp"
+#include "profile.hpp"
 
 namespace ct {
 namespace {
@@ -172,6 +173,16 @@ hipError_t dispatch_storage(const ct_nf4_weight *w, void *out, int out_dtype, in
 
 bool valid_dtype(int d) { return d == CT_F32 || d == CT_F16 || d == CT_BF16; }
 
+// Algorithmic HBM bytes of one decode: packed nibbles, first-level scales, second-level
+// scales, the code books and the offset read once, and the output written once.
+double dequant_bytes(const ct_nf4_weight *w, int64_t n, int out_dtype) {
+    const int64_t nb = cdiv(n, w->blocksize);
+    double bytes = (double)((n + 1) / 2) + 16 * 4;
+    bytes += w->nested ? (double)nb + 4.0 * cdiv(nb, w->blocksize2) + 256 * 4 + 4 : 4.0 * nb;
+    bytes += (double)n * (out_dtype == CT_F32 ? 4 : 2);
+    return bytes;
+}
+
 }  // namespace
 
 // Host-side validation shared with the GEMM entry points.
@@ -202,7 +213,9 @@ extern "C" int ct_nf4_dequant(const ct_nf4_weight *w, void *out, int32_t out_dty
     const bool vec = (n % 8 == 0) && w->blocksize >= 8 &&
                      (reinterpret_cast<uintptr_t>(w->packed) % 4 == 0) &&
                      (reinterpret_cast<uintptr_t>(out) % 16 == 0);
+    const int slot = profile_open(CT_PROF_DEQUANT, stream);
     hipError_t e = w->nested ? dispatch_storage<true>(w, out, out_dtype, n, lb, lb2, vec, stream)
                              : dispatch_storage<false>(w, out, out_dtype, n, lb, lb2, vec, stream);
+    profile_close(slot, stream, dequant_bytes(w, n, out_dtype));
     return e == hipSuccess ? 0 : (int)e;
 }

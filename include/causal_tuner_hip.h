@@ -173,6 +173,25 @@ int ct_accumulate(float *out, int64_t ldo,
                   int64_t p, int64_t q, int64_t j, int32_t add,
                   void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Kernel timing for benchmarks; no counterpart in the reference (which publishes no kernel
+ * timings). ct_profile_begin enables the families in `families` and creates `capacity`
+ * HIP event pairs; each later launch of an enabled family is bracketed by one pair
+ * recorded on the launch stream (launches beyond capacity go untimed). ct_profile_read
+ * synchronises on those events and returns, for the launches of `family` (a mask), their
+ * summed duration (ms), their count and their summed algorithmic work: FLOPs for the GEMM
+ * families, HBM bytes for the decoder. ct_profile_end stops timing and frees the events.
+ * One profiler at a time; the timed launches may come from any thread.
+ */
+#define CT_PROF_FWD_GEMM 1  /* fused projection GEMM of ct_forward_linear: 2 m n (k + r) */
+#define CT_PROF_DX_GEMM  2  /* fused projection GEMM of ct_input_gradient: 2 m k (n + r) */
+#define CT_PROF_DEQUANT  4  /* ct_nf4_dequant: packed + scale + code bytes read, output written */
+#define CT_PROF_PARAM    8  /* ct_parameter_gradients (dA and dB): 2 m r (k + n) */
+#define CT_PROF_LOWRANK 16  /* xa = x a^T and low = dy b inside the entry points: 2 m r k or 2 m r n */
+int ct_profile_begin(int32_t families, int32_t capacity);
+int ct_profile_read(int32_t family, double *total_ms, int64_t *launches, double *work);
+int ct_profile_end(void);
+
 #ifdef __cplusplus
 }
 #endif
