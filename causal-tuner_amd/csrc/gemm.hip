@@ -31,6 +31,9 @@
 // Workgroup ids are remapped so each of the 8 XCDs walks a contiguous, M-grouped range of
 // output tiles: the workgroups that share an L2 also share A and B panels.
 
+#include <cstdio>
+#include <cstdlib>
+
 #include "common.hpp"
 #include "profile.hpp"
 
@@ -80,9 +83,13 @@ struct GemmParams {
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0, 0, 0, 0); }
 
 // LDS slot of chunk `chunk` (0..7) of tile row `row`; SWZ_DIV rows share a swizzle value.
+// With v = row / SWZ_DIV the 16-byte chunk moves to position chunk ^ ((v ^ v / 8) % 8):
+// the 16 rows of an MFMA fragment read (consecutive v) land on distinct positions in each
+// half, and so do the rows 8 apart that the transposing loaders write together.
 template <int SWZ_DIV>
 __device__ __forceinline__ int slot(int row, int chunk) {
-    return row * 8 + (chunk ^ ((row / SWZ_DIV) & 7));
+    const int v = row / SWZ_DIV;
+    return row * 8 + (chunk ^ ((v ^ (v >> 3)) & 7));
 }
 
 // Eight nibbles of one packed dword -> eight bf16 (element 2j from the high nibble of byte j).
@@ -411,7 +418,8 @@ struct Fast<SRC_KC, ROWS, SWZ_DIV, THREADS> {
 #pragma unroll
         for (int i = 0; i < kInstr; ++i) {
             const int row = (wave * kInstr + i) * 8 + (lane >> 3);
-            const int c = (lane & 7) ^ ((row / SWZ_DIV) & 7);
+            const int v = row / SWZ_DIV;
+            const int c = (lane & 7) ^ ((v ^ (v >> 3)) & 7);
             kc[i] = c * 8;
             off[i] = (uint32_t)((row * o.ld + c * 8) * 2);
         }
@@ -970,6 +978,17 @@ hipError_t run(Problem &pr, hipStream_t s) {
 // Tile and split count for a reduction-heavy GEMM with a small output (dA, dB): enough
 // workgroups for about one per CU, at least 8 k-tiles per split, at most 32 splits.
 void choose_reduction(int64_t m, int64_t n, int64_t kred, int *tile, int *splits) {
+#ifdef CT_TUNING
+    if (const char *env = getenv("CT_RED")) {
+        int t = 1, sp = 4;
+        if (sscanf(env, "%d,%d", &t, &sp) == 2) {
+            *tile = t;
+            const int64_t ktiles = cdiv(kred, kBK);
+            *splits = (int)(sp < 1 ? 1 : (sp > ktiles ? ktiles : sp));
+            return;
+        }
+    }
+#endif
     *tile = (m >= 128 && n >= 128) ? TILE_128 : TILE_64;
     const int64_t e = kTileEdge[*tile];
     const int64_t tiles_out = cdiv(m, e) * cdiv(n, e);
