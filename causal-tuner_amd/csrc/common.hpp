@@ -31,8 +31,13 @@ __device__ __forceinline__ uint16_t bf16_bits(float v) {
     __bf16 h = (__bf16)v;
     return __builtin_bit_cast(uint16_t, h);
 }
+// Two values -> one dword of bf16 (lo in the low half), as one v_cvt_pk_bf16_f32: the
+// scalar form converts each value separately and re-packs them with a shift and an OR.
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return (uint32_t)bf16_bits(lo) | ((uint32_t)bf16_bits(hi) << 16);
+    const f32x2_v f = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_v));
 }
 __device__ __forceinline__ float bf16_to_f32(uint16_t bits) {
     return __builtin_bit_cast(float, (uint32_t)bits << 16);

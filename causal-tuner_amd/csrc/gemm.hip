@@ -547,7 +547,8 @@ struct Fast<SRC_NF4, ROWS, SWZ_DIV, THREADS> {
                                            float offset) const {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const float s = ok[i] ? lcode2[qa[i] & 255u] * a2[i] + offset : 0.f;
+            const float decoded = lcode2[qa[i] & 255u] * a2[i] + offset;  // read unconditionally: no branch
+            const float s = ok[i] ? decoded : 0.f;
             const int c0 = half[i] * 4;
             stage[slot<SWZ_DIV>(row[i], c0 + 0)] = nf4_decode8(q[i].x, s, lcode);
             stage[slot<SWZ_DIV>(row[i], c0 + 1)] = nf4_decode8(q[i].y, s, lcode);
@@ -608,7 +609,10 @@ struct Fast<SRC_NF4T, ROWS, SWZ_DIV, THREADS> {
                                            float offset) const {
         float s[R];
 #pragma unroll
-        for (int i = 0; i < R; ++i) s[i] = ok[i] ? lcode2[qa[i] & 255u] * a2[i] + offset : 0.f;
+        for (int i = 0; i < R; ++i) {
+            const float decoded = lcode2[qa[i] & 255u] * a2[i] + offset;  // read unconditionally: no branch
+            s[i] = ok[i] ? decoded : 0.f;
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int shift = (j & 1) ? 8 * (j >> 1) : 8 * (j >> 1) + 4;
@@ -669,7 +673,9 @@ struct FastRunner {
 #pragma unroll
                     for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
             }
+#ifndef CT_INTERLEAVE_COMMIT
             __builtin_amdgcn_sched_barrier(0);
+#endif
             la.commit(nxt, lcode, lcode2, off_a);
             lb.commit(nxt + BM * 8, lcode, lcode2, off_b);
             __builtin_amdgcn_s_waitcnt(0);
