@@ -103,7 +103,12 @@ def time_events(fn, iters, warmup=3):
 
 
 def dequant_measure(device):
-    """C2: standalone NF4 dequant of [28672, 8192] (and [8192, 8192]) to bf16, HBM GB/s."""
+    """C2: standalone NF4 dequant of [28672, 8192] (and [8192, 8192]) to bf16, HBM GB/s.
+
+    Each launch is timed with HIP events around the kernel (ct_profile_*); the byte count
+    per launch is the decoder's algorithmic traffic (packed + scales + code books read,
+    bf16 output written). Several copies rotate when one would fit the 256 MB Infinity Cache."""
+    from causal_tuner.kernels import _native
     from causal_tuner.kernels.nf4_cuda import dequantize_nf4_into
     from causal_tuner.quant.nf4 import quantize_nf4
     results = {}
@@ -117,16 +122,20 @@ def dequant_measure(device):
             packed, state = quantize_nf4(w)
             del w
             weights.append((packed, state, torch.empty(rows, cols, device=device, dtype=torch.bfloat16)))
-        index = [0]
-
-        def run():
-            packed, state, out = weights[index[0] % copies]
-            index[0] += 1
+        for i in range(3):  # warm-up
+            packed, state, out = weights[i % copies]
             dequantize_nf4_into(packed, state, out)
-        ms = time_events(run, 30)
-        gbs = moved / (ms * 1e-3) / 1e9
+        torch.cuda.synchronize()
+        with _native.KernelTimer(_native.CT_PROF_DEQUANT, capacity=64) as timer:
+            for i in range(30):
+                packed, state, out = weights[i % copies]
+                dequantize_nf4_into(packed, state, out)
+            ms_total, launches, work = timer.read(_native.CT_PROF_DEQUANT)
+        ms = ms_total / launches
+        gbs = work / launches / (ms * 1e-3) / 1e9
         results[f"{rows}x{cols}"] = {"GB/s": round(gbs, 1), "avg_us": round(ms * 1e3, 2), "bytes": int(moved),
-                                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+                                     "frac": round(gbs / HBM_PEAK_GBS, 4), "launches": launches,
+                                     "copies": copies}
         del weights
     return results
 
