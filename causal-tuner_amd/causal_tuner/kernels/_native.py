@@ -38,11 +38,15 @@ _SIGNATURES = {
     "ct_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "ct_nf4_dequant": (ctypes.c_int, [ctypes.POINTER(NF4Weight), _P, _I32, _P]),
     "ct_nf4_fused_supported": (ctypes.c_int, [ctypes.POINTER(NF4Weight)]),
-    "ct_gemm": (ctypes.c_int, [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _P, _I32, _I64, _I64, _I64, _P]),
+    "ct_gemm_workspace": (_I64, [_I64, _I64, _I64, _I32, _I32, _I32]),
+    "ct_gemm": (ctypes.c_int, [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _P, _I32, _I64, _I64, _I64, _P, _I64,
+                               _P]),
+    "ct_forward_linear_workspace": (_I64, [_I64, _I64, _I64, _I64]),
     "ct_forward_linear": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _P, _I64, _P,
-                                         _I64, _I64, _I64, _I64, _P]),
+                                         _I64, _I64, _I64, _I64, _P, _I64, _P]),
+    "ct_input_gradient_workspace": (_I64, [_I64, _I64, _I64, _I64]),
     "ct_input_gradient": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _I64, _P,
-                                         _I64, _I64, _I64, _I64, _I32, _P]),
+                                         _I64, _I64, _I64, _I64, _I32, _P, _I64, _P]),
     "ct_parameter_gradients_workspace": (_I64, [_I64, _I64, _I64, _I64]),
     "ct_parameter_gradients": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32,
                                               _P, _I64, _P]),

@@ -62,6 +62,8 @@ def _operand(t):
 
 
 def _workspace(nbytes, device):
+    """Caller-owned scratch for split reductions (the kernels never allocate); torch's
+    caching allocator makes the per-call allocation cheap."""
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
@@ -150,11 +152,13 @@ def _forward(x, weight, state, a, b, bias, out, xa):
     bias = None if bias is None else bias.contiguous()
     target, low = _Output(out), _Contiguous(xa)
     desc = None if state is None else _native.nf4_descriptor(w, state)
+    lib = _native.library()
+    ws = _workspace(lib.ct_forward_linear_workspace(m, n, k, r), x.device)
     with torch.cuda.device(x.device):
-        status = _native.library().ct_forward_linear(
+        status = lib.ct_forward_linear(
             _native.ptr(x), ldx, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),
             _native.ptr(b), _native.ptr(bias), _native.ptr(target.buffer), target.ld, _native.ptr(low.buffer),
-            m, n, k, r, _native.stream_of(x))
+            m, n, k, r, _native.ptr(ws), ws.numel(), _native.stream_of(x))
     _native.check(status, "ct_forward_linear")
     target.finish()
     low.finish()
@@ -181,11 +185,13 @@ def _input_gradient(dy, weight, state, a, b, dx, low, add):
     if add and target.buffer is not dx:
         target.buffer.copy_(dx)
     desc = None if state is None else _native.nf4_descriptor(w, state)
+    lib = _native.library()
+    ws = _workspace(lib.ct_input_gradient_workspace(m, n, k, r), dy.device)
     with torch.cuda.device(dy.device):
-        status = _native.library().ct_input_gradient(
+        status = lib.ct_input_gradient(
             _native.ptr(dy), lddy, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),
             _native.ptr(b), _native.ptr(target.buffer), target.ld, _native.ptr(lowc.buffer), m, n, k, r, int(add),
-            _native.stream_of(dy))
+            _native.ptr(ws), ws.numel(), _native.stream_of(dy))
     _native.check(status, "ct_input_gradient")
     target.finish()
     lowc.finish()
@@ -353,10 +359,12 @@ def _low_rank(x, factor, out, *, transpose):
     x, ldx = _rows(x)
     factor = factor.contiguous()
     target = _Output(out)
+    lib = _native.library()
+    ws = _workspace(lib.ct_gemm_workspace(m, r, k, 0, int(transpose), _native.CT_BF16), x.device)
     with torch.cuda.device(x.device):
-        status = _native.library().ct_gemm(_native.ptr(x), ldx, 0, _native.ptr(factor),
-                                           k if transpose else r, int(transpose), _native.ptr(target.buffer),
-                                           target.ld, _native.CT_BF16, None, 0, m, r, k, _native.stream_of(x))
+        status = lib.ct_gemm(_native.ptr(x), ldx, 0, _native.ptr(factor), k if transpose else r, int(transpose),
+                             _native.ptr(target.buffer), target.ld, _native.CT_BF16, None, 0, m, r, k,
+                             _native.ptr(ws), ws.numel(), _native.stream_of(x))
     _native.check(status, "ct_gemm")
     target.finish()
 

@@ -34,7 +34,7 @@
 #include <cstdio>
 #include <cstdlib>
 
-#include "common.hpp"
+#include "gemm_common.hpp"
 #include "profile.hpp"
 
 namespace ct {
@@ -48,61 +48,6 @@ constexpr int kThreads = 256;  // 4 wavefronts per workgroup
 constexpr int kXcds = 8;       // MI355X dispatches workgroups round-robin over 8 XCDs
 constexpr int kGroupM = 8;     // m-tiles per group in the L2-friendly tile order
 
-enum Src { SRC_KC = 0, SRC_KS = 1, SRC_NF4 = 2, SRC_NF4T = 3 };
-
-struct Operand {
-    const void *p;        // bf16 elements, or packed NF4 bytes
-    int64_t ld;           // bf16: row pitch in elements; NF4: columns of the dense weight
-    const void *absmax;   // NF4: u8 codes (nested) or f32 scales
-    const float *absmax2; // NF4 nested: second-level scales
-    const float *offset;  // NF4 nested: scalar offset
-    int32_t lb, lb2;      // NF4: log2 of the first- and second-level block sizes
-    int32_t nested;
-};
-
-struct Segment {
-    Operand a, b;
-    int64_t k;  // reduction extent
-};
-
-struct GemmParams {
-    Segment seg[2];
-    int nseg;
-    int64_t m, n;
-    void *c;
-    int64_t ldc;
-    int64_t split_stride;     // elements between split partial outputs (blockIdx.z)
-    int64_t tiles_per_split;  // k-tiles handled by one blockIdx.z
-    const uint16_t *bias;     // bf16 [n] or null
-    int beta;                 // add the existing C
-    int tiles_m, tiles_n;
-    const float *code;        // NF4 code book [16]
-    const float *code2;       // NF4 second-level code book [256]
-};
-
-__device__ __forceinline__ uint4 zero4() { return make_uint4(0, 0, 0, 0); }
-
-// LDS slot of chunk `chunk` (0..7) of tile row `row`; SWZ_DIV rows share a swizzle value.
-// With v = row / SWZ_DIV the 16-byte chunk moves to position chunk ^ ((v ^ v / 8) % 8):
-// the 16 rows of an MFMA fragment read (consecutive v) land on distinct positions in each
-// half, and so do the rows 8 apart that the transposing loaders write together.
-template <int SWZ_DIV>
-__device__ __forceinline__ int slot(int row, int chunk) {
-    const int v = row / SWZ_DIV;
-    return row * 8 + (chunk ^ ((v ^ (v >> 3)) & 7));
-}
-
-// Eight nibbles of one packed dword -> eight bf16 (element 2j from the high nibble of byte j).
-__device__ __forceinline__ uint4 nf4_decode8(uint32_t d, float s, const float *lds_code) {
-    float v[8];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        v[2 * b] = lds_code[(d >> (8 * b + 4)) & 15u] * s;
-        v[2 * b + 1] = lds_code[(d >> (8 * b)) & 15u] * s;
-    }
-    return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                      pack_bf16x2(v[6], v[7]));
-}
 
 // ------------------------------------------------------------------ operand tile loaders
 // ROWS: output-dimension extent of the tile. SWZ_DIV: rows that share one swizzle value.
@@ -365,32 +310,8 @@ struct SegmentRunner {
 // buffer loads: the hardware range check returns zeros past num_records, and an invalid
 // lane is pointed past the range, so the k-loop body has no branches and the compiler can
 // interleave loads, LDS traffic, NF4 decoding and MFMA within one basic block.
-typedef __attribute__((address_space(3))) void lds_void_t;
-constexpr uint32_t kOOB = 0x80000000u;  // a byte offset beyond every buffer range used here
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int64_t bytes) {
-    const int64_t clamped = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes);
-    // 0x00020000: the raw 32-bit data format word used for gfx9 buffer descriptors.
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)clamped, 0x00020000);
-}
-
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
-__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-}
-__device__ __forceinline__ uint32_t buf_load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
-}
-
 template <int SRC, int ROWS, int SWZ_DIV, int THREADS>
 struct Fast;
-
-// Pack elements (half h) of dwords lo and hi into one dword: lo's in the low half.
-__device__ __forceinline__ uint32_t pick16(uint32_t hi, uint32_t lo, int h) {
-    return __builtin_amdgcn_perm(hi, lo, h ? 0x07060302u : 0x05040100u);
-}
 
 // KC: each wave instruction moves 64 x 16 bytes = 8 tile rows x 8 chunks; lane l owns slot
 // base + l (row l/8, physical chunk l%8), so it fetches the global chunk that the swizzle
@@ -857,6 +778,8 @@ struct Problem {
     bool vec;
     int splits;
     int tile;     // forced tile, or -1 to choose
+    void *ws;     // caller's workspace for few-row split reductions (may be null)
+    int64_t ws_bytes;
 };
 
 // Byte extent of a dense operand whose output-dimension extent is `rows`.
@@ -955,6 +878,14 @@ hipError_t run(Problem &pr, hipStream_t s) {
     if (p.nseg == 1) {
         pr.src[2] = pr.src[0];
         pr.src[3] = pr.src[1];
+    }
+    if (pr.splits == 1 && pr.out == CT_BF16 && p.m <= 64) {
+        // Few rows: the workgroup streams the weight with its 8 waves splitting the reduction.
+        const int sa[2] = {pr.src[0], pr.src[2]}, sb[2] = {pr.src[1], pr.src[3]};
+        if (skinny_supported(p, sa, sb, pr.out)) {
+            const hipError_t e = skinny_run(p, sb, pr.ws, pr.ws_bytes, s);
+            if (e != hipErrorNotSupported) return e;
+        }
     }
     const int tile = pr.tile >= 0 ? pr.tile : choose_tile(p.m, p.n, pr.splits);
     const int64_t tiles = total_tiles(p);
@@ -1059,6 +990,18 @@ hipError_t run_reduction(Problem pr, void *out, int64_t ldo, int add, void *ws, 
 
 int to_status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
 
+// Workspace a few-row problem can use (0 when it takes the tiled kernels). Only the
+// shapes and source kinds matter, so the operands need not exist yet.
+int64_t problem_workspace(int64_t m, int64_t n, const int64_t k[2], int nseg, const int src_b[2]) {
+    if (m < 1 || m > 64 || n < 1) return 0;
+    GemmParams p{};
+    p.m = m;
+    p.n = n;
+    p.nseg = nseg;
+    for (int s = 0; s < nseg; ++s) p.seg[s].k = k[s];
+    return skinny_workspace_bytes(p, src_b);
+}
+
 int log2_of(int64_t v) {
     if (v <= 0 || (v & (v - 1))) return -1;
     int l = 0;
@@ -1117,9 +1060,17 @@ extern "C" const char *ct_status_string(int status) {
 
 extern "C" int ct_nf4_fused_supported(const ct_nf4_weight *w) { return nf4_fusable(w) ? 1 : 0; }
 
+extern "C" int64_t ct_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t trans_a, int32_t trans_b,
+                                     int32_t c_dtype) {
+    if (trans_a || c_dtype != CT_BF16) return 0;
+    const int64_t ks[2] = {k, 0};
+    const int sb[2] = {trans_b ? SRC_KC : SRC_KS, trans_b ? SRC_KC : SRC_KS};
+    return problem_workspace(m, n, ks, 1, sb);
+}
+
 extern "C" int ct_gemm(const void *a, int64_t lda, int32_t trans_a, const void *b, int64_t ldb, int32_t trans_b,
                        void *c, int64_t ldc, int32_t c_dtype, const void *bias, int32_t beta, int64_t m, int64_t n,
-                       int64_t k, hipStream_t stream) {
+                       int64_t k, void *workspace, int64_t workspace_bytes, hipStream_t stream) {
     if (m < 0 || n < 0 || k < 0) return -CT_EINVAL_SHAPE;
     if (c_dtype != CT_BF16 && c_dtype != CT_F32) return -CT_EINVAL_DTYPE;
     if (m == 0 || n == 0) return 0;
@@ -1141,13 +1092,24 @@ extern "C" int ct_gemm(const void *a, int64_t lda, int32_t trans_a, const void *
     pr.out = c_dtype;
     pr.splits = 1;
     pr.tile = -1;
+    pr.ws = workspace;
+    pr.ws_bytes = workspace ? workspace_bytes : 0;
     pr.vec = vec_ok(pr);
     return to_status(run(pr, stream));
 }
 
+extern "C" int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, int64_t r) {
+    const int64_t inner = ct_gemm_workspace(m, r, k, 0, 1, CT_BF16);
+    const int64_t ks[2] = {k, r};
+    const int sb[2] = {SRC_NF4, SRC_KC};  // the dense weight (KC) has the same split shape
+    const int64_t main = problem_workspace(m, n, ks, r > 0 ? 2 : 1, sb);
+    return inner > main ? inner : main;  // the two launches run in order on one stream
+}
+
 extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense, const ct_nf4_weight *w_nf4,
                                  const void *a, const void *b, const void *bias, void *out, int64_t ldo, void *xa,
-                                 int64_t m, int64_t n, int64_t k, int64_t r, hipStream_t stream) {
+                                 int64_t m, int64_t n, int64_t k, int64_t r, void *workspace, int64_t workspace_bytes,
+                                 hipStream_t stream) {
     if (m < 0 || n < 0 || k < 0 || r < 0) return -CT_EINVAL_SHAPE;
     if (m == 0 || n == 0) return 0;
     if (!x || !out || (!w_dense == !w_nf4) || (r > 0 && (!a || !b || !xa))) return -CT_EINVAL_POINTER;
@@ -1161,7 +1123,8 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
     if (r > 0) {
         // xa = x a^T  (NT, bf16 out)
         const int slot = profile_open(CT_PROF_LOWRANK, stream);
-        const int st = ct_gemm(x, ldx, 0, a, k, 1, xa, r, CT_BF16, nullptr, 0, m, r, k, stream);
+        const int st = ct_gemm(x, ldx, 0, a, k, 1, xa, r, CT_BF16, nullptr, 0, m, r, k, workspace, workspace_bytes,
+                               stream);
         profile_close(slot, stream, 2.0 * m * r * k);
         if (st) return st;
     }
@@ -1188,6 +1151,8 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
     pr.out = CT_BF16;
     pr.splits = 1;
     pr.tile = -1;
+    pr.ws = workspace;
+    pr.ws_bytes = workspace ? workspace_bytes : 0;
     pr.vec = vec_ok(pr);
     const int slot = profile_open(CT_PROF_FWD_GEMM, stream);
     const hipError_t e = run(pr, stream);
@@ -1195,9 +1160,18 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
     return to_status(e);
 }
 
+extern "C" int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, int64_t r) {
+    const int64_t inner = ct_gemm_workspace(m, r, n, 0, 0, CT_BF16);
+    const int64_t ks[2] = {n, r};
+    const int sb[2] = {SRC_NF4T, SRC_KS};
+    const int64_t main = problem_workspace(m, k, ks, r > 0 ? 2 : 1, sb);
+    return inner > main ? inner : main;
+}
+
 extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_dense, const ct_nf4_weight *w_nf4,
                                  const void *a, const void *b, void *dx, int64_t lddx, void *low, int64_t m,
-                                 int64_t n, int64_t k, int64_t r, int32_t add, hipStream_t stream) {
+                                 int64_t n, int64_t k, int64_t r, int32_t add, void *workspace,
+                                 int64_t workspace_bytes, hipStream_t stream) {
     if (m < 0 || n < 0 || k < 0 || r < 0) return -CT_EINVAL_SHAPE;
     if (m == 0 || k == 0) return 0;
     if (!dy || !dx || (!w_dense == !w_nf4) || (r > 0 && (!a || !b || !low))) return -CT_EINVAL_POINTER;
@@ -1211,7 +1185,8 @@ extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_den
     if (r > 0) {
         // low = dy b  (NN, bf16 out)
         const int slot = profile_open(CT_PROF_LOWRANK, stream);
-        const int st = ct_gemm(dy, lddy, 0, b, r, 0, low, r, CT_BF16, nullptr, 0, m, r, n, stream);
+        const int st = ct_gemm(dy, lddy, 0, b, r, 0, low, r, CT_BF16, nullptr, 0, m, r, n, workspace,
+                               workspace_bytes, stream);
         profile_close(slot, stream, 2.0 * m * r * n);
         if (st) return st;
     }
@@ -1237,6 +1212,8 @@ extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_den
     pr.out = CT_BF16;
     pr.splits = 1;
     pr.tile = -1;
+    pr.ws = workspace;
+    pr.ws_bytes = workspace ? workspace_bytes : 0;
     pr.vec = vec_ok(pr);
     const int slot = profile_open(CT_PROF_DX_GEMM, stream);
     const hipError_t e = run(pr, stream);

@@ -1,0 +1,105 @@
+// Operand descriptors and device helpers shared by the projection GEMM kernels
+// (gemm.hip: tiled MFMA GEMMs; skinny.hip: few-row GEMMs).
+#pragma once
+
+#include "common.hpp"
+
+namespace ct {
+
+enum Src { SRC_KC = 0, SRC_KS = 1, SRC_NF4 = 2, SRC_NF4T = 3 };
+
+struct Operand {
+    const void *p;        // bf16 elements, or packed NF4 bytes
+    int64_t ld;           // bf16: row pitch in elements; NF4: columns of the dense weight
+    const void *absmax;   // NF4: u8 codes (nested) or f32 scales
+    const float *absmax2; // NF4 nested: second-level scales
+    const float *offset;  // NF4 nested: scalar offset
+    int32_t lb, lb2;      // NF4: log2 of the first- and second-level block sizes
+    int32_t nested;
+};
+
+struct Segment {
+    Operand a, b;
+    int64_t k;  // reduction extent
+};
+
+struct GemmParams {
+    Segment seg[2];
+    int nseg;
+    int64_t m, n;
+    void *c;
+    int64_t ldc;
+    int64_t split_stride;     // elements between split partial outputs (blockIdx.z)
+    int64_t tiles_per_split;  // k-tiles handled by one blockIdx.z
+    const uint16_t *bias;     // bf16 [n] or null
+    int beta;                 // add the existing C
+    int tiles_m, tiles_n;
+    const float *code;        // NF4 code book [16]
+    const float *code2;       // NF4 second-level code book [256]
+    float *split_ws;          // few-row kernels: fp32 split partials [splits][m][n]
+};
+
+// ------------------------------------------------------------------ LDS layout and NF4 decode
+__device__ __forceinline__ uint4 zero4() { return make_uint4(0, 0, 0, 0); }
+
+// LDS slot of chunk `chunk` (0..7) of tile row `row`; SWZ_DIV rows share a swizzle value.
+// With v = row / SWZ_DIV the 16-byte chunk moves to position chunk ^ ((v ^ v / 8) % 8):
+// the 16 rows of an MFMA fragment read (consecutive v) land on distinct positions in each
+// half, and so do the rows 8 apart that the transposing loaders write together.
+template <int SWZ_DIV>
+__device__ __forceinline__ int slot(int row, int chunk) {
+    const int v = row / SWZ_DIV;
+    return row * 8 + (chunk ^ ((v ^ (v >> 3)) & 7));
+}
+
+// Eight nibbles of one packed dword -> eight bf16 (element 2j from the high nibble of byte j).
+__device__ __forceinline__ uint4 nf4_decode8(uint32_t d, float s, const float *lds_code) {
+    float v[8];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        v[2 * b] = lds_code[(d >> (8 * b + 4)) & 15u] * s;
+        v[2 * b + 1] = lds_code[(d >> (8 * b)) & 15u] * s;
+    }
+    return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                      pack_bf16x2(v[6], v[7]));
+}
+
+// ------------------------------------------------------------------ buffer loads
+// Raw buffer loads: the hardware range check returns zeros past num_records, and an
+// invalid lane is pointed past the range, so loops over k need no branches.
+typedef __attribute__((address_space(3))) void lds_void_t;
+constexpr uint32_t kOOB = 0x80000000u;  // a byte offset beyond every buffer range used here
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int64_t bytes) {
+    const int64_t clamped = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes);
+    // 0x00020000: the raw 32-bit data format word used for gfx9 buffer descriptors.
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)clamped, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+}
+
+// Pack elements (half h) of dwords lo and hi into one dword: lo's in the low half.
+__device__ __forceinline__ uint32_t pick16(uint32_t hi, uint32_t lo, int h) {
+    return __builtin_amdgcn_perm(hi, lo, h ? 0x07060302u : 0x05040100u);
+}
+
+constexpr bool is_nf4_src(int src) { return src == SRC_NF4 || src == SRC_NF4T; }
+
+// Few-row GEMMs (skinny.hip): C[m, n] for m <= 64 with activation operands A (reduction-
+// contiguous bf16) and B of any source. Returns hipErrorNotSupported when the problem is
+// outside what the skinny kernels take (the caller then uses the tiled kernels).
+// With `ws` (fp32, ws_bytes) the reduction may be split across workgroups (partials summed
+// in split order); skinny_workspace_bytes() is the size that allows the preferred split.
+hipError_t skinny_run(GemmParams p, const int src_b[2], void *ws, int64_t ws_bytes, hipStream_t stream);
+int64_t skinny_workspace_bytes(const GemmParams &p, const int src_b[2]);
+bool skinny_supported(const GemmParams &p, const int src_a[2], const int src_b[2], int out_dtype);
+
+}  // namespace ct

@@ -95,11 +95,18 @@ int ct_nf4_dequant(const ct_nf4_weight *w, void *out, int32_t out_dtype, hipStre
  *   A(m,k) = a[m*lda + k]  (trans_a = 0)  or  a[k*lda + m]  (trans_a = 1)
  *   B(k,n) = b[n*ldb + k]  (trans_b = 1)  or  b[k*ldb + n]  (trans_b = 0)
  * c_dtype is CT_BF16 (rounded once, RTNE) or CT_F32. bias may be null (bf16 [n]).
+ *
+ * Workspace (here and in ct_forward_linear / ct_input_gradient): with m <= 64 rows the
+ * reduction may be split across workgroups, the fp32 partials going to the caller's
+ * workspace and summed in a fixed order (results do not depend on timing). The *_workspace
+ * query gives the size that allows the preferred split; a null or smaller workspace is
+ * valid and only splits less (no split at all without one).
  */
+int64_t ct_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t trans_a, int32_t trans_b, int32_t c_dtype);
 int ct_gemm(const void *a, int64_t lda, int32_t trans_a,
             const void *b, int64_t ldb, int32_t trans_b,
             void *c, int64_t ldc, int32_t c_dtype, const void *bias, int32_t beta,
-            int64_t m, int64_t n, int64_t k, hipStream_t stream);
+            int64_t m, int64_t n, int64_t k, void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * 1 when the fused NF4 operand of ct_forward_linear / ct_input_gradient accepts `w`:
@@ -123,11 +130,13 @@ int ct_nf4_fused_supported(const ct_nf4_weight *w);
  * x [m, k] (ldx), a bf16 [r, k], b bf16 [n, r], bias bf16 [n] or null, out [m, n] (ldo),
  * xa bf16 [m, r] contiguous.
  */
+int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, int64_t r);
 int ct_forward_linear(const void *x, int64_t ldx,
                       const void *w_dense, const ct_nf4_weight *w_nf4,
                       const void *a, const void *b, const void *bias,
                       void *out, int64_t ldo, void *xa,
-                      int64_t m, int64_t n, int64_t k, int64_t r, hipStream_t stream);
+                      int64_t m, int64_t n, int64_t k, int64_t r,
+                      void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * Replaces input_gradient (kernels/linear.py:36-39):
@@ -137,12 +146,13 @@ int ct_forward_linear(const void *x, int64_t ldx,
  * transposed layout this product needs), a bf16 [r, k], b bf16 [n, r], dx [m, k] (lddx),
  * low bf16 [m, r] contiguous.
  */
+int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, int64_t r);
 int ct_input_gradient(const void *dy, int64_t lddy,
                       const void *w_dense, const ct_nf4_weight *w_nf4,
                       const void *a, const void *b,
                       void *dx, int64_t lddx, void *low,
                       int64_t m, int64_t n, int64_t k, int64_t r, int32_t add,
-                      hipStream_t stream);
+                      void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * Replaces parameter_gradients (kernels/linear.py:42-44) with accumulate's fp32 branch

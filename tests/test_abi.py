@@ -76,11 +76,17 @@ def test_host_side_argument_errors_return_negative_status():
     desc.blocksize = 64
     assert lib.ct_nf4_dequant(ctypes.byref(desc), ctypes.c_void_p(16), 7, null) == -3
     # negative sizes and short leading dimensions
-    assert lib.ct_gemm(16, 4, 0, 16, 4, 1, 16, 4, _native.CT_BF16, null, 0, -1, 4, 4, null) == -2
-    assert lib.ct_gemm(16, 2, 0, 16, 4, 1, 16, 4, _native.CT_BF16, null, 0, 4, 4, 4, null) == -2
-    assert lib.ct_gemm(16, 4, 0, 16, 4, 1, 16, 4, 9, null, 0, 4, 4, 4, null) == -3
+    assert lib.ct_gemm(16, 4, 0, 16, 4, 1, 16, 4, _native.CT_BF16, null, 0, -1, 4, 4, null, 0, null) == -2
+    assert lib.ct_gemm(16, 2, 0, 16, 4, 1, 16, 4, _native.CT_BF16, null, 0, 4, 4, 4, null, 0, null) == -2
+    assert lib.ct_gemm(16, 4, 0, 16, 4, 1, 16, 4, 9, null, 0, 4, 4, 4, null, 0, null) == -3
     # empty problems are no-ops
-    assert lib.ct_gemm(null, 0, 0, null, 0, 1, null, 0, _native.CT_BF16, null, 0, 0, 0, 0, null) == 0
+    assert lib.ct_gemm(null, 0, 0, null, 0, 1, null, 0, _native.CT_BF16, null, 0, 0, 0, 0, null, 0, null) == 0
+    # few-row problems ask for split workspace; large ones and fp32 outputs do not
+    assert lib.ct_gemm_workspace(16, 256, 6144, 0, 1, _native.CT_BF16) > 0
+    assert lib.ct_gemm_workspace(8192, 256, 4096, 0, 1, _native.CT_BF16) == 0
+    assert lib.ct_gemm_workspace(16, 256, 6144, 0, 1, _native.CT_F32) == 0
+    assert lib.ct_input_gradient_workspace(16, 24576, 6144, 256) > 0
+    assert lib.ct_forward_linear_workspace(8192, 4096, 4096, 256) == 0
     # workspace too small for a split reduction
     need = lib.ct_accumulate_workspace(256, 4096, 8192)
     assert need > 0

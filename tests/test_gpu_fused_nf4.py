@@ -16,9 +16,11 @@ from oracle import lora as olora
 
 pytestmark = pytest.mark.gpu
 
-# (m, k, n, r): tails in every dimension, odd ranks, and 256x256-tile shapes.
+# (m, k, n, r): tails in every dimension, odd ranks, and 256x256-tile shapes; m <= 64 runs
+# the few-row kernels (1, 2 and 4 row blocks; 1, 2 and 4 column blocks per workgroup).
 SHAPES = [(37, 96, 80, 8), (300, 256, 192, 5), (1, 64, 64, 4), (513, 1024, 1032, 16), (4096, 4096, 4096, 256),
-          (2048, 4096, 11008, 256), (4096, 11008, 4096, 64)]
+          (2048, 4096, 11008, 256), (4096, 11008, 4096, 64), (16, 6144, 24576, 256), (64, 24576, 6144, 256),
+          (5, 1024, 512, 8), (29, 2048, 16384, 16), (64, 4096, 8192, 128), (3, 128, 8200, 4)]
 
 
 def _weight(n, k, blocksize=64, nested=True, dtype=torch.bfloat16, seed=0):

@@ -52,7 +52,7 @@ def test_gemm_layouts_and_tails(m, n, k, trans_a, trans_b, out):
     bias = (torch.randn(n, device="cuda") * 0.5).to(torch.bfloat16)
     c = torch.full((m, n), float("nan"), device="cuda", dtype=out)
     status = lib.ct_gemm(abase.data_ptr(), lda, trans_a, bbase.data_ptr(), ldb, trans_b, c.data_ptr(), n,
-                         _native.dtype_code(out), bias.data_ptr(), 0, m, n, k, _native.stream_of(c))
+                         _native.dtype_code(out), bias.data_ptr(), 0, m, n, k, None, 0, _native.stream_of(c))
     assert status == 0
     want = a.double() @ b.double() + bias.double()
     worst, norm = _err(c, want)
@@ -60,7 +60,7 @@ def test_gemm_layouts_and_tails(m, n, k, trans_a, trans_b, out):
     assert worst <= tol and norm <= tol / 2, (worst, norm)
     # beta accumulation on top of the previous result, no bias
     status = lib.ct_gemm(abase.data_ptr(), lda, trans_a, bbase.data_ptr(), ldb, trans_b, c.data_ptr(), n,
-                         _native.dtype_code(out), None, 1, m, n, k, _native.stream_of(c))
+                         _native.dtype_code(out), None, 1, m, n, k, None, 0, _native.stream_of(c))
     assert status == 0
     worst, norm = _err(c, want + a.double() @ b.double())
     assert worst <= 2 * tol and norm <= tol, (worst, norm)
@@ -109,6 +109,31 @@ def test_gemm_runs_on_the_callers_stream():
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         assert lib.ct_gemm(a.data_ptr(), 512, 0, a.data_ptr(), 512, 1, c.data_ptr(), 512, _native.CT_F32, None, 0,
-                           512, 512, 512, ctypes.c_void_p(stream.cuda_stream)) == 0
+                           512, 512, 512, None, 0, ctypes.c_void_p(stream.cuda_stream)) == 0
     torch.cuda.current_stream().wait_stream(stream)
     torch.testing.assert_close(c, (a.float() @ a.float().T), rtol=1e-4, atol=1e-3)
+
+
+@pytest.mark.parametrize("m,n,k,trans_b", [(16, 256, 6144, 1), (7, 256, 24576, 0), (64, 128, 4096, 1),
+                                           (33, 512, 2048, 0)])
+def test_few_row_split_reduction_is_deterministic(m, n, k, trans_b):
+    """m <= 64 with a workspace splits the reduction across workgroups; the fp32 partials
+    add in split order, so repeated calls agree bit for bit, and the result matches a
+    float64 product of the same bf16 operands within bf16 rounding."""
+    lib = _native.library()
+    a, abase, lda = _operand(m, k, False)
+    b, bbase, ldb = _operand(k, n, bool(trans_b))
+    need = lib.ct_gemm_workspace(m, n, k, 0, trans_b, _native.CT_BF16)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    outs = []
+    for workspace, size in ((ws.data_ptr(), need), (ws.data_ptr(), need), (None, 0)):
+        c = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+        assert lib.ct_gemm(abase.data_ptr(), lda, 0, bbase.data_ptr(), ldb, trans_b, c.data_ptr(), n,
+                           _native.CT_BF16, None, 0, m, n, k, workspace, size, _native.stream_of(c)) == 0
+        outs.append(c)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    want = a.double() @ b.double()
+    for c in (outs[0], outs[2]):
+        worst, norm = _err(c, want)
+        assert worst <= 8e-3 and norm <= 4e-3, (worst, norm)
