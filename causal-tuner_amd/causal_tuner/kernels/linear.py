@@ -130,6 +130,9 @@ def accumulate(output, left, right, *, add=True):
 
 
 def forward_linear(x, weight, a, b, *, out, xa, bias=None):
+    if isinstance(weight, _Base):  # a frozen base as the GEMMs consume it (packed NF4 or dense)
+        weight.forward(x, a, b, bias, out, xa)
+        return
     if not x.is_cuda:
         if bias is None:
             torch.mm(x, weight.T, out=out)
@@ -165,6 +168,9 @@ def _forward(x, weight, state, a, b, bias, out, xa):
 
 
 def input_gradient(dy, weight, a, b, dx, low, *, add=False):
+    if isinstance(weight, _Base):
+        weight.input_gradient(dy, a, b, dx, low, add)
+        return
     if not dy.is_cuda:
         torch.mm(dy, b, out=low)
         torch.addmm(dx, dy, weight, beta=1 if add else 0, out=dx)

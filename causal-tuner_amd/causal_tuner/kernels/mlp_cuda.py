@@ -1,0 +1,179 @@
+"""Tiled LoRA MLP with the SiLU-multiply and a graph-free analytic backward, on gfx950.
+
+Same operator API as the reference's kernels/mlp_cuda.py: `activation` (10-35, the Triton
+`_activation` kernel, here `ct_silu_multiply`), `_SiLUMultiply` / `silu_multiply` (38-55),
+`_forward_into` (58-81), `_TiledLoRAMLP` (84-143) and `tiled_lora_mlp` (146-161). Gate, up and
+down are NF4-LoRA projections on the helpers of kernels/linear.py; a packed NF4 base stays
+packed (the GEMMs decode it in LDS) instead of being materialised per call.
+"""
+
+import torch
+
+from . import _native
+from .linear import _Base, forward_linear, input_gradient, parameter_gradients, projection_parameters, _low_rank
+
+
+def _silu(gate, up, h, dg, du, backward, reconstruct):
+    tensors = [t for t in (gate, up, h, dg, du) if t is not None]
+    if not all(t.is_cuda and t.is_contiguous() and t.dtype == gate.dtype for t in tensors):
+        raise ValueError("activation expects contiguous device tensors of one dtype")
+    code = _native.dtype_code(gate.dtype)
+    if code == _native.CT_F16:
+        raise NotImplementedError("activation: the HIP kernel takes bfloat16 or float32")
+    with torch.cuda.device(gate.device):
+        status = _native.library().ct_silu_multiply(
+            _native.ptr(gate), _native.ptr(up), _native.ptr(h), _native.ptr(dg), _native.ptr(du), gate.numel(),
+            int(backward), int(reconstruct), code, _native.stream_of(gate))
+    _native.check(status, "ct_silu_multiply")
+
+
+def activation(gate, up, gradient=None, *, out=None):
+    """h = dtype(silu(gate)) * up (reference mlp_cuda.py:28-35). With `gradient`, the
+    backward in place: gate <- d gate, up <- d up, gradient <- h."""
+    if gradient is not None:
+        out = gradient
+    elif out is None:
+        out = torch.empty_like(gate)
+    if gradient is not None:
+        _silu(gate, up, out, gate, up, True, True)
+    else:
+        _silu(gate, up, out, None, None, False, True)
+    return out
+
+
+class _SiLUMultiply(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gate, up):
+        gate, up = gate.contiguous(), up.contiguous()
+        ctx.save_for_backward(gate, up)
+        return activation(gate, up)
+
+    @staticmethod
+    def backward(ctx, grad):
+        gate, up = ctx.saved_tensors
+        dg, du = torch.empty_like(gate), torch.empty_like(up)
+        _silu(gate, up, grad.contiguous(), dg, du, True, False)
+        return dg, du
+
+
+def silu_multiply(gate, up):
+    return _SiLUMultiply.apply(gate, up)
+
+
+def _bases(parameters, states, dtype):
+    return [_Base(parameters[4*i], state, dtype) for i, state in enumerate(states)]
+
+
+@torch.no_grad()
+def _forward_into(output, x, dtype, tile, states, parameters, residual, *, save=False):
+    flat = x.reshape(-1, x.shape[-1]).to(dtype)
+    matrices = _bases(parameters, states, dtype)
+    adapters = [(parameters[4*i+1].to(dtype), parameters[4*i+2].to(dtype)) for i in range(3)]
+    rows = min(tile, len(flat))
+    width = matrices[0].rows
+    workspace = torch.empty((1 if save else 2, rows, width), device=x.device, dtype=dtype)
+    low = torch.empty((rows, max(len(a) for a, _ in adapters)), device=x.device, dtype=dtype)
+    saved = (() if not save else (
+        *(torch.empty((len(flat), width), device=x.device, dtype=dtype) for _ in range(2)),
+        *(torch.empty((len(flat), len(a)), device=x.device, dtype=dtype) for a, _ in adapters[:2])))
+    destination = output.view_as(flat)
+    for start in range(0, len(flat), tile):
+        part = flat[start:start+tile]
+        gate, up = ((buffer[start:start+len(part)] for buffer in saved[:2]) if save
+                    else (buffer[:len(part)] for buffer in workspace))
+        xa = [low[:len(part), :len(a)] for a, _ in adapters]
+        if save:
+            xa[:2] = [buffer[start:start+len(part)] for buffer in saved[2:]]
+        forward_linear(part, matrices[0], *adapters[0], out=gate, xa=xa[0])
+        forward_linear(part, matrices[1], *adapters[1], out=up, xa=xa[1])
+        hidden = activation(gate, up, out=workspace[0, :len(part)] if save else gate)
+        forward_linear(hidden, matrices[2], *adapters[2], out=destination[start:start+tile], xa=xa[2])
+    if residual is not None:
+        output.add_(residual)
+    return saved
+
+
+class _TiledLoRAMLP(torch.autograd.Function):
+    """Saves only the input and the parameters (plus, in cache mode, gate/up and their xa);
+    the backward recomputes gate/up per tile and never builds an autograd graph."""
+
+    @staticmethod
+    def forward(ctx, x, dtype, tile, states, residual, cache, *parameters):
+        ctx.dtype, ctx.tile, ctx.states = dtype, tile, states
+        ctx.cache = cache
+        if cache:
+            output = torch.empty(x.shape, device=x.device, dtype=dtype)
+            saved = _forward_into(output, x, dtype, tile, states, parameters, residual, save=True)
+            ctx.save_for_backward(x, *saved, *parameters)
+            return output
+        # Register the saved inputs before the wrapper fills this private output, so a
+        # checkpoint replay can stop before the GEMMs (reference mlp_cuda.py:94-97).
+        ctx.save_for_backward(x, *parameters)
+        return torch.empty(x.shape, device=x.device, dtype=dtype)
+
+    @staticmethod
+    def backward(ctx, grad):
+        x, *parameters = ctx.saved_tensors
+        saved = parameters[:4] if ctx.cache else ()
+        if ctx.cache:
+            parameters = parameters[4:]
+        residual_grad = grad if ctx.needs_input_grad[4] else None
+        flat = x.reshape(-1, x.shape[-1]).to(ctx.dtype)
+        grad = grad.reshape_as(flat).to(ctx.dtype)
+        dx = torch.empty_like(flat) if ctx.needs_input_grad[0] else None
+        matrices = _bases(parameters, ctx.states, ctx.dtype)
+        adapters = [(parameters[4*i+1].to(ctx.dtype), parameters[4*i+2].to(ctx.dtype)) for i in range(3)]
+        allocate = torch.empty_like if len(flat) else torch.zeros_like
+        gradients = [(allocate(parameters[4*i+1]), allocate(parameters[4*i+2])) for i in range(3)]
+        rows = min(ctx.tile, len(flat))
+        workspace = torch.empty((3, rows, matrices[0].rows), device=x.device, dtype=ctx.dtype)
+        low_inputs = [torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype) for a, _ in adapters]
+        low_grad = torch.empty((rows, max(len(a) for a, _ in adapters)), device=x.device, dtype=ctx.dtype)
+        for start in range(0, len(flat), ctx.tile):
+            part, dy = flat[start:start+ctx.tile], grad[start:start+ctx.tile]
+            gate, up, dh = (buffer[:len(part)] for buffer in workspace)
+            xa = [buffer[:len(part)] for buffer in low_inputs]
+            low = [low_grad[:len(part), :len(a)] for a, _ in adapters]
+            if ctx.cache:
+                # The activation backward overwrites its tile buffers: copy only this tile so
+                # the saved values survive a repeated backward.
+                gate.copy_(saved[0][start:start+len(part)])
+                up.copy_(saved[1][start:start+len(part)])
+                xa[:2] = [value[start:start+len(part)] for value in saved[2:]]
+            else:
+                forward_linear(part, matrices[0], *adapters[0], out=gate, xa=xa[0])
+                forward_linear(part, matrices[1], *adapters[1], out=up, xa=xa[1])
+            input_gradient(dy, matrices[2], *adapters[2], dh, low[2])
+            # Reuse the three wide tile buffers: (gate, up, dh) -> (d gate, d up, hidden).
+            hidden = activation(gate, up, dh)
+            _low_rank(hidden, adapters[2][0], xa[2], transpose=True)
+            parameter_gradients(hidden, dy, *gradients[2], low[2], xa[2], add=start > 0)
+            for index, signal in enumerate((gate, up)):
+                if dx is not None:
+                    input_gradient(signal, matrices[index], *adapters[index], dx[start:start+ctx.tile], low[index],
+                                   add=index > 0)
+                else:
+                    _low_rank(signal, adapters[index][1], low[index], transpose=False)
+                parameter_gradients(part, signal, *gradients[index], low[index], xa[index], add=start > 0)
+        result = [value for da, db in gradients for value in (None, da, db, None)]
+        return (None if dx is None else dx.reshape_as(x).to(x.dtype), None, None, None, residual_grad, None, *result)
+
+
+def tiled_lora_mlp(module, x, residual=None, *, tile=None, cache=None):
+    """`module` carries gate_proj, up_proj, down_proj (Projection), tile and
+    cache_intermediates, as the reference's MLP (modeling/model.py:111-139) does."""
+    modules = (module.gate_proj, module.up_proj, module.down_proj)
+    dtype = modules[0].compute_dtype
+    if residual is not None and (residual.shape != x.shape or residual.dtype != dtype):
+        return tiled_lora_mlp(module, x, tile=tile, cache=cache)+residual
+    parameters, states = [], []
+    for projection in modules:
+        values, state = projection_parameters(projection)
+        parameters.extend(values)
+        states.append(state)
+    tile = (module.tile if tile is None else tile) or max(1, x.numel()//x.shape[-1])
+    cache = (module.cache_intermediates if cache is None else cache) and torch.is_grad_enabled()
+    output = _TiledLoRAMLP.apply(x, dtype, tile, tuple(states), residual, cache, *parameters)
+    if not cache:
+        _forward_into(output, x, dtype, tile, states, parameters, residual)
+    return output

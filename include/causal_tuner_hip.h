@@ -23,6 +23,7 @@
  *   kernels/linear.py:42-44     parameter_gradients        -> ct_parameter_gradients
  *   kernels/linear.py:84,125    torch.mm(x, a.T, out=xa)   -> ct_gemm (NT, bf16 out)
  *   kernels/linear.py:124,167   torch.mm(dy, b, out=low)   -> ct_gemm (NN, bf16 out)
+ *   kernels/mlp_cuda.py:10-35   _activation (SiLU x up)    -> ct_silu_multiply
  */
 #ifndef CAUSAL_TUNER_HIP_H
 #define CAUSAL_TUNER_HIP_H
@@ -182,6 +183,20 @@ int ct_accumulate(float *out, int64_t ldo,
                   const void *right, int64_t ldr, int32_t trans_r,
                   int64_t p, int64_t q, int64_t j, int32_t add,
                   void *workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Replaces the SiLU-multiply kernel `_activation` (kernels/mlp_cuda.py:10-35) of the
+ * tiled LoRA MLP, elementwise over n elements of `dtype` (CT_BF16 or CT_F32), fp32 math:
+ *   sig = 1 / (1 + exp(-gate)),  act = dtype(gate * sig)
+ *   reconstruct:  h = act * up
+ *   backward:     dgate = dtype(h * up) * sig * (1 + gate * (1 - sig)),  dup = h * act
+ * (in backward, h holds the incoming gradient; with reconstruct it is overwritten by the
+ * hidden activation). The outputs may alias the inputs as the reference's backward call
+ * does (dgate = gate, dup = up). Results match the reference within float rounding: the
+ * exponential is this library's, not Triton's.
+ */
+int ct_silu_multiply(const void *gate, const void *up, void *h, void *dgate, void *dup, int64_t n,
+                     int32_t backward, int32_t reconstruct, int32_t dtype, hipStream_t stream);
 
 /*
  * Kernel timing for benchmarks; no counterpart in the reference (which publishes no kernel

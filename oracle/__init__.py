@@ -12,5 +12,7 @@ Contents (each function cites the reference file:line it restates):
   lora.py         the reference's torch-op sequence for one projection (CPU, bf16) and a
                   float64-accumulated oracle with the reference's bf16 rounding points for
                   xa and low and one final rounding of out and dx.
+  mlp.py          the tiled LoRA MLP (SiLU-multiply with its bf16 rounding points, gate/up/
+                  down projections, analytic backward) in float64.
   nf4_dequant.c   plain-C decode, the timed CPU baseline (built by oracle/Makefile).
 """
