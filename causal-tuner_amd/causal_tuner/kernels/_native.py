@@ -41,10 +41,10 @@ _SIGNATURES = {
     "ct_gemm_workspace": (_I64, [_I64, _I64, _I64, _I32, _I32, _I32]),
     "ct_gemm": (ctypes.c_int, [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _P, _I32, _I64, _I64, _I64, _P, _I64,
                                _P]),
-    "ct_forward_linear_workspace": (_I64, [_I64, _I64, _I64, _I64]),
+    "ct_forward_linear_workspace": (_I64, [_I64, _I64, _I64, _I64, _I32]),
     "ct_forward_linear": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _P, _I64, _P,
                                          _I64, _I64, _I64, _I64, _P, _I64, _P]),
-    "ct_input_gradient_workspace": (_I64, [_I64, _I64, _I64, _I64]),
+    "ct_input_gradient_workspace": (_I64, [_I64, _I64, _I64, _I64, _I32]),
     "ct_input_gradient": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _I64, _P,
                                          _I64, _I64, _I64, _I64, _I32, _P, _I64, _P]),
     "ct_parameter_gradients_workspace": (_I64, [_I64, _I64, _I64, _I64]),

@@ -50,14 +50,16 @@ constexpr int kGroupM = 8;     // m-tiles per group in the L2-friendly tile orde
 
 
 // ------------------------------------------------------------------ operand tile loaders
-// ROWS: output-dimension extent of the tile. SWZ_DIV: rows that share one swizzle value.
+// ROWS: output-dimension extent of the tile. FRAG: output columns per lane of the MFMA
+// fragments that read the tile (1 for the A side, FN for the B side); tile row n is
+// stored at LDS row frag_row<FRAG>(n).
 // load() issues the global reads of k-tile k0 into registers; store() writes the tile to
 // LDS (decoding NF4 on the way).
-template <int SRC, int ROWS, bool VEC, int SWZ_DIV>
+template <int SRC, int ROWS, bool VEC, int FRAG>
 struct Loader;
 
-template <int ROWS, bool VEC, int SWZ_DIV>
-struct Loader<SRC_KC, ROWS, VEC, SWZ_DIV> {
+template <int ROWS, bool VEC, int FRAG>
+struct Loader<SRC_KC, ROWS, VEC, FRAG> {
     static constexpr int kPer = (ROWS * 8 + kThreads - 1) / kThreads;
     uint4 r[kPer];
     __device__ __forceinline__ void load(const Operand &o, int64_t rows, int64_t kext, int64_t r0, int64_t k0,
@@ -84,13 +86,13 @@ struct Loader<SRC_KC, ROWS, VEC, SWZ_DIV> {
         for (int i = 0; i < kPer; ++i) {
             const int id = tid + i * kThreads;
             if (id >= ROWS * 8) break;
-            lds[slot<SWZ_DIV>(id >> 3, id & 7)] = r[i];
+            lds[slot(frag_row<FRAG>(id >> 3), id & 7)] = r[i];
         }
     }
 };
 
-template <int ROWS, bool VEC, int SWZ_DIV>
-struct Loader<SRC_KS, ROWS, VEC, SWZ_DIV> {
+template <int ROWS, bool VEC, int FRAG>
+struct Loader<SRC_KS, ROWS, VEC, FRAG> {
     // ROWS/8 row blocks x 8 k-chunks = ROWS blocks of 8x8, at most one per lane.
     uint4 r[8];
     __device__ __forceinline__ void load(const Operand &o, int64_t rows, int64_t kext, int64_t r0, int64_t k0,
@@ -119,15 +121,15 @@ struct Loader<SRC_KS, ROWS, VEC, SWZ_DIV> {
         const int row = (tid % (ROWS / 8)) * 8;
         const int chunk = tid / (ROWS / 8);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) lds[slot<SWZ_DIV>(row + j, chunk)] = t[j];
+        for (int j = 0; j < 8; ++j) lds[slot(frag_row<FRAG>(row + j), chunk)] = t[j];
     }
 };
 
 // NF4 weight [rows][cols], reduction along cols (forward: x w^T). One unit = 32 elements
 // of one row: 16 packed bytes inside one first-level block (blocksize >= 32, cols % 32 == 0).
 // load() fetches the packed bytes and the block's scale code; store() decodes.
-template <int ROWS, bool VEC, int SWZ_DIV>
-struct Loader<SRC_NF4, ROWS, VEC, SWZ_DIV> {
+template <int ROWS, bool VEC, int FRAG>
+struct Loader<SRC_NF4, ROWS, VEC, FRAG> {
     static constexpr int kUnits = ROWS * 2;
     static constexpr int kPer = (kUnits + kThreads - 1) / kThreads;
     uint4 q[kPer];
@@ -169,10 +171,10 @@ struct Loader<SRC_NF4, ROWS, VEC, SWZ_DIV> {
             float s = a2[i];
             if (nested) s = qa[i] < 256 ? lcode2[qa[i]] * a2[i] + offset : 0.f;
             const int row = id >> 1, c0 = (id & 1) * 4;
-            lds[slot<SWZ_DIV>(row, c0 + 0)] = nf4_decode8(q[i].x, s, lcode);
-            lds[slot<SWZ_DIV>(row, c0 + 1)] = nf4_decode8(q[i].y, s, lcode);
-            lds[slot<SWZ_DIV>(row, c0 + 2)] = nf4_decode8(q[i].z, s, lcode);
-            lds[slot<SWZ_DIV>(row, c0 + 3)] = nf4_decode8(q[i].w, s, lcode);
+            lds[slot(frag_row<FRAG>(row), c0 + 0)] = nf4_decode8(q[i].x, s, lcode);
+            lds[slot(frag_row<FRAG>(row), c0 + 1)] = nf4_decode8(q[i].y, s, lcode);
+            lds[slot(frag_row<FRAG>(row), c0 + 2)] = nf4_decode8(q[i].z, s, lcode);
+            lds[slot(frag_row<FRAG>(row), c0 + 3)] = nf4_decode8(q[i].w, s, lcode);
         }
     }
 };
@@ -180,8 +182,8 @@ struct Loader<SRC_NF4, ROWS, VEC, SWZ_DIV> {
 // NF4 weight [rows][cols], reduction along rows (the transposed use in dx = dy w). One
 // unit = 8 weight rows x 8 weight columns (one packed dword per row), at most one per lane;
 // the decoded values are written straight into the reduction-contiguous LDS layout.
-template <int ROWS, bool VEC, int SWZ_DIV>
-struct Loader<SRC_NF4T, ROWS, VEC, SWZ_DIV> {
+template <int ROWS, bool VEC, int FRAG>
+struct Loader<SRC_NF4T, ROWS, VEC, FRAG> {
     static constexpr int kCB = ROWS / 8;  // 8-column blocks across the tile
     uint32_t d[8];
     float a2[8];
@@ -231,7 +233,7 @@ struct Loader<SRC_NF4T, ROWS, VEC, SWZ_DIV> {
             float v[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = lcode[(d[i] >> shift) & 15u] * s[i];
-            lds[slot<SWZ_DIV>(col + j, chunk)] = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+            lds[slot(frag_row<FRAG>(col + j), chunk)] = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
                                                             pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
         }
     }
@@ -253,12 +255,11 @@ template <int BM, int BN, int SA, int SB, bool VEC>
 struct SegmentRunner {
     static constexpr int WM = BM / 2, WN = BN / 2;  // 2 x 2 waves
     static constexpr int FM = WM / 16, FN = WN / 16;
-    static constexpr int kStage = (BM + BN) * 8;    // uint4 slots per pipeline stage
 
     __device__ __forceinline__ static void run(const Segment &sg, int64_t m, int64_t n, int64_t m0, int64_t n0,
-                                               int64_t tbeg, int64_t tend, f32x4 (&acc)[FM][FN], uint4 *lds,
-                                               const float *lcode, const float *lcode2, int tid, int wm0,
-                                               int wn0) {
+                                               int64_t tbeg, int64_t tend, f32x4 (&acc)[FM][FN], uint4 *lds0,
+                                               uint4 *lds1, const float *lcode, const float *lcode2, int tid,
+                                               int wm0, int wn0) {
         if (tbeg >= tend) return;
         const int lane = tid & 63;
         Loader<SA, BM, VEC, 1> la;
@@ -268,8 +269,8 @@ struct SegmentRunner {
         la.load(sg.a, m, sg.k, m0, tbeg * kBK, tid);
         lb.load(sg.b, n, sg.k, n0, tbeg * kBK, tid);
         __syncthreads();  // every wave is done with the buffers of a previous segment
-        store_tile<decltype(la), SA>(la, lds, tid, lcode, lcode2, sg.a.nested, off_a);
-        store_tile<decltype(lb), SB>(lb, lds + BM * 8, tid, lcode, lcode2, sg.b.nested, off_b);
+        store_tile<decltype(la), SA>(la, lds0, tid, lcode, lcode2, sg.a.nested, off_a);
+        store_tile<decltype(lb), SB>(lb, lds0 + BM * 8, tid, lcode, lcode2, sg.b.nested, off_b);
         __syncthreads();
         for (int64_t t = tbeg; t < tend; ++t) {
             const int buf = (int)((t - tbeg) & 1);
@@ -278,16 +279,16 @@ struct SegmentRunner {
                 la.load(sg.a, m, sg.k, m0, (t + 1) * kBK, tid);
                 lb.load(sg.b, n, sg.k, n0, (t + 1) * kBK, tid);
             }
-            const uint4 *sa = lds + buf * kStage;
+            const uint4 *sa = buf ? lds1 : lds0;
             const uint4 *sb = sa + BM * 8;
 #pragma unroll
             for (int ks = 0; ks < kBK / 32; ++ks) {
                 const int chunk = ks * 4 + (lane >> 4);
                 uint4 af[FM], bf[FN];
 #pragma unroll
-                for (int i = 0; i < FM; ++i) af[i] = sa[slot<1>(wm0 + i * 16 + (lane & 15), chunk)];
+                for (int i = 0; i < FM; ++i) af[i] = sa[slot(wm0 + i * 16 + (lane & 15), chunk)];
 #pragma unroll
-                for (int j = 0; j < FN; ++j) bf[j] = sb[slot<FN>(wn0 + (lane & 15) * FN + j, chunk)];
+                for (int j = 0; j < FN; ++j) bf[j] = sb[slot(wn0 + j * 16 + (lane & 15), chunk)];
 #pragma unroll
                 for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -295,7 +296,7 @@ struct SegmentRunner {
             }
             __builtin_amdgcn_sched_barrier(0);  // keep the next tile's stores after the MFMA block
             if (more) {
-                uint4 *next = lds + (buf ^ 1) * kStage;
+                uint4 *next = buf ? lds0 : lds1;
                 store_tile<decltype(la), SA>(la, next, tid, lcode, lcode2, sg.a.nested, off_a);
                 store_tile<decltype(lb), SB>(lb, next + BM * 8, tid, lcode, lcode2, sg.b.nested, off_b);
             }
@@ -310,19 +311,20 @@ struct SegmentRunner {
 // buffer loads: the hardware range check returns zeros past num_records, and an invalid
 // lane is pointed past the range, so the k-loop body has no branches and the compiler can
 // interleave loads, LDS traffic, NF4 decoding and MFMA within one basic block.
-template <int SRC, int ROWS, int SWZ_DIV, int THREADS>
+template <int SRC, int ROWS, int FRAG, int THREADS>
 struct Fast;
 
 // KC: each wave instruction moves 64 x 16 bytes = 8 tile rows x 8 chunks; lane l owns slot
 // base + l (row l/8, physical chunk l%8), so it fetches the global chunk that the swizzle
-// maps to that physical position. By default the chunk goes global -> VGPR -> ds_write;
-// with CT_KC_DMA it goes global -> LDS directly (buffer_load ... lds). Measured on MI355X
-// at M=8192 the register path is 5-20% faster (the DMA form needs an M0 write per wave
-// instruction and completes behind the same vmcnt as the operand loads).
-template <int ROWS, int SWZ_DIV, int THREADS>
-struct Fast<SRC_KC, ROWS, SWZ_DIV, THREADS> {
+// maps to that physical position. The chunk goes global -> VGPR -> ds_write: measured on
+// MI355X at M=8192 this beat loading straight into LDS (buffer_load ... lds) by 5-20%, as
+// the LDS form needs an M0 write per wave instruction and must complete before the barrier
+// that publishes the stage, while register staging lets the loads run across it.
+template <int ROWS, int FRAG, int THREADS>
+struct Fast<SRC_KC, ROWS, FRAG, THREADS> {
     static constexpr int kWaves = THREADS / 64;
     static constexpr int kInstr = ROWS / (8 * kWaves);
+    static constexpr int kVmem = kInstr, kWrites = kInstr;  // per tile, per lane
     static_assert(kInstr >= 1, "tile too small for the workgroup");
     __amdgpu_buffer_rsrc_t r;
     uint32_t off[kInstr];  // byte offset of the lane's chunk at k0 = 0
@@ -338,14 +340,13 @@ struct Fast<SRC_KC, ROWS, SWZ_DIV, THREADS> {
         const int lane = tid & 63;
 #pragma unroll
         for (int i = 0; i < kInstr; ++i) {
-            const int row = (wave * kInstr + i) * 8 + (lane >> 3);
-            const int v = row / SWZ_DIV;
-            const int c = (lane & 7) ^ ((v ^ (v >> 3)) & 7);
+            int srow, c;
+            slot_coords((wave * kInstr + i) * 64 + lane, srow, c);
+            const int row = frag_row_inv<FRAG>(srow);
             kc[i] = c * 8;
             off[i] = (uint32_t)((row * o.ld + c * 8) * 2);
         }
     }
-#ifndef CT_KC_DMA
     uint4 v[kInstr];
     __device__ __forceinline__ void issue(uint4 *, int64_t k0) {
 #pragma unroll
@@ -359,17 +360,6 @@ struct Fast<SRC_KC, ROWS, SWZ_DIV, THREADS> {
 #pragma unroll
         for (int i = 0; i < kInstr; ++i) stage[(wave * kInstr + i) * 64 + lane] = v[i];
     }
-#else
-    __device__ __forceinline__ void issue(uint4 *stage, int64_t k0) {
-#pragma unroll
-        for (int i = 0; i < kInstr; ++i) {
-            const uint32_t o = ((int)k0 + kc[i] < kext) ? off[i] + (uint32_t)(k0 * 2) : kOOB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(stage + (wave * kInstr + i) * 64), 16, o, 0,
-                                                     0, 0);
-        }
-    }
-    __device__ __forceinline__ void commit(uint4 *, const float *, const float *, float) const {}
-#endif
 };
 
 // Store R bf16 values (R/2 dwords) at byte offset `byte` of the stage.
@@ -383,10 +373,11 @@ __device__ __forceinline__ void store_part(uint4 *stage, int byte, const uint32_
 
 // KS: 8x8 blocks (8 reduction rows x 8 output rows), split over LPB lanes that take
 // R = 8 / LPB reduction rows each; transposed in registers, R values per LDS write.
-template <int ROWS, int SWZ_DIV, int THREADS>
-struct Fast<SRC_KS, ROWS, SWZ_DIV, THREADS> {
+template <int ROWS, int FRAG, int THREADS>
+struct Fast<SRC_KS, ROWS, FRAG, THREADS> {
     static constexpr int kLPB = THREADS / ROWS;
     static constexpr int R = 8 / kLPB;
+    static constexpr int kVmem = R, kWrites = 8;
     static_assert(kLPB >= 1 && kLPB <= 4, "unsupported tile / workgroup ratio");
     __amdgpu_buffer_rsrc_t r;
     uint32_t off0, pitch;
@@ -416,16 +407,17 @@ struct Fast<SRC_KS, ROWS, SWZ_DIV, THREADS> {
             uint32_t w[R / 2];
 #pragma unroll
             for (int q = 0; q < R / 2; ++q) w[q] = pick16(d[(2 * q + 1) * 4 + (j >> 1)], d[(2 * q) * 4 + (j >> 1)], j & 1);
-            store_part<R>(stage, slot<SWZ_DIV>(col + j, chunk) * 16 + h * R * 2, w);
+            store_part<R>(stage, slot(frag_row<FRAG>(col + j), chunk) * 16 + h * R * 2, w);
         }
     }
 };
 
 // NF4 (nested), reduction along the weight's columns: units of 32 elements of one row.
-template <int ROWS, int SWZ_DIV, int THREADS>
-struct Fast<SRC_NF4, ROWS, SWZ_DIV, THREADS> {
+template <int ROWS, int FRAG, int THREADS>
+struct Fast<SRC_NF4, ROWS, FRAG, THREADS> {
     static constexpr int kUnits = ROWS * 2;
     static constexpr int kPer = (kUnits + THREADS - 1) / THREADS;
+    static constexpr int kVmem = 3 * kPer, kWrites = 4 * kPer;
     __amdgpu_buffer_rsrc_t rq, ra, r2;
     uint32_t e0[kPer];  // element index of the unit at k0 = 0 (whole weight)
     int row[kPer], half[kPer];
@@ -471,21 +463,22 @@ struct Fast<SRC_NF4, ROWS, SWZ_DIV, THREADS> {
             const float decoded = lcode2[qa[i] & 255u] * a2[i] + offset;  // read unconditionally: no branch
             const float s = ok[i] ? decoded : 0.f;
             const int c0 = half[i] * 4;
-            stage[slot<SWZ_DIV>(row[i], c0 + 0)] = nf4_decode8(q[i].x, s, lcode);
-            stage[slot<SWZ_DIV>(row[i], c0 + 1)] = nf4_decode8(q[i].y, s, lcode);
-            stage[slot<SWZ_DIV>(row[i], c0 + 2)] = nf4_decode8(q[i].z, s, lcode);
-            stage[slot<SWZ_DIV>(row[i], c0 + 3)] = nf4_decode8(q[i].w, s, lcode);
+            stage[slot(frag_row<FRAG>(row[i]), c0 + 0)] = nf4_decode8(q[i].x, s, lcode);
+            stage[slot(frag_row<FRAG>(row[i]), c0 + 1)] = nf4_decode8(q[i].y, s, lcode);
+            stage[slot(frag_row<FRAG>(row[i]), c0 + 2)] = nf4_decode8(q[i].z, s, lcode);
+            stage[slot(frag_row<FRAG>(row[i]), c0 + 3)] = nf4_decode8(q[i].w, s, lcode);
         }
     }
 };
 
 // NF4 (nested), reduction along the weight's rows: units of 8 weight rows x 8 columns,
 // split over LPB lanes that take R = 8 / LPB weight rows each.
-template <int ROWS, int SWZ_DIV, int THREADS>
-struct Fast<SRC_NF4T, ROWS, SWZ_DIV, THREADS> {
+template <int ROWS, int FRAG, int THREADS>
+struct Fast<SRC_NF4T, ROWS, FRAG, THREADS> {
     static constexpr int kCB = ROWS / 8;
     static constexpr int kLPB = THREADS / ROWS;
     static constexpr int R = 8 / kLPB;
+    static constexpr int kVmem = 3 * R, kWrites = 8;
     static_assert(kLPB >= 1 && kLPB <= 4, "unsupported tile / workgroup ratio");
     __amdgpu_buffer_rsrc_t rq, ra, r2;
     uint32_t e0;  // element index of (weight row chunk*8 + h*R, column r0 + col) at k0 = 0
@@ -542,8 +535,45 @@ struct Fast<SRC_NF4T, ROWS, SWZ_DIV, THREADS> {
             for (int q = 0; q < R / 2; ++q)
                 w[q] = pack_bf16x2(lcode[(d[2 * q] >> shift) & 15u] * s[2 * q],
                                    lcode[(d[2 * q + 1] >> shift) & 15u] * s[2 * q + 1]);
-            store_part<R>(stage, slot<SWZ_DIV>(col + j, chunk) * 16 + h * R * 2, w);
+            store_part<R>(stage, slot(frag_row<FRAG>(col + j), chunk) * 16 + h * R * 2, w);
         }
+    }
+};
+
+#ifndef CT_PV
+#define CT_PV 2
+#endif
+// Instruction-group order for one k-step of FastRunner (LLVM's sched_group_barrier masks:
+// 0x8 MFMA, 0x20 VMEM read, 0x100 DS read, 0x200 DS write). The A fragments and the first
+// column's B fragments are read first; after that every column's MFMAs carry the next
+// column's B reads and a share of the stage writes and global loads for later tiles.
+template <int FM, int FN, int KS, class LA, class LB>
+struct SchedPattern {
+    static constexpr int kW = LA::kWrites + LB::kWrites, kV = LA::kVmem + LB::kVmem;
+    static constexpr int kWper = (kW + FN - 1) / FN, kVper = (kV + FN - 1) / FN;
+    template <int J>
+    __device__ __forceinline__ static void column() {
+        if constexpr (J < FN) {
+            constexpr int w = kW - J * kWper < kWper ? (kW - J * kWper > 0 ? kW - J * kWper : 0) : kWper;
+            constexpr int v = kV - J * kVper < kVper ? (kV - J * kVper > 0 ? kV - J * kVper : 0) : kVper;
+            constexpr int mf = FM * KS;
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if constexpr (J + 1 < FN) __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);
+            if constexpr (w > 0) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x200, w, 0);
+            }
+            if constexpr (v > 0) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, v, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, mf - 1 - (w > 0) - (v > 0), 0);
+            column<J + 1>();
+        }
+    }
+    __device__ __forceinline__ static void emit() {
+        __builtin_amdgcn_sched_group_barrier(0x100, KS * FM + KS, 0);
+        column<0>();
     }
 };
 
@@ -552,56 +582,71 @@ struct FastRunner {
     static constexpr int THREADS = 64 * WAVES_M * WAVES_N;
     static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     static constexpr int FM = WM / 16, FN = WN / 16;
-    static constexpr int kStage = (BM + BN) * 8;
+    static constexpr int KS = kBK / 32;
+    using LA = Fast<SA, BM, 1, THREADS>;
+    using LB = Fast<SB, BN, FN, THREADS>;
+
+    // One k-step: MFMAs over stage `cur` while the registers' tile goes into stage `nxt`
+    // and the loads of the tile after it are issued. The two stages are distinct LDS
+    // arrays, so the compiler knows the stage writes never alias the fragment reads and
+    // can interleave them with the MFMAs.
+    __device__ __forceinline__ static void step(LA &la, LB &lb, const uint4 *cur, uint4 *nxt, int64_t knext,
+                                                f32x4 (&acc)[FM][FN], const float *lcode, const float *lcode2,
+                                                float off_a, float off_b, int lane, int wm0, int wn0) {
+        uint4 af[KS][FM];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int i = 0; i < FM; ++i) af[ks][i] = cur[slot(wm0 + i * 16 + (lane & 15), ks * 4 + (lane >> 4))];
+        la.commit(nxt, lcode, lcode2, off_a);
+        lb.commit(nxt + BM * 8, lcode, lcode2, off_b);
+        la.issue(nxt, knext);
+        lb.issue(nxt + BM * 8, knext);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            uint4 bf[KS];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                bf[ks] = cur[BM * 8 + slot(wn0 + j * 16 + (lane & 15), ks * 4 + (lane >> 4))];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int i = 0; i < FM; ++i) acc[i][j] = mfma16x16x32(af[ks][i], bf[ks], acc[i][j]);
+        }
+#if CT_PV == 2
+        SchedPattern<FM, FN, KS, LA, LB>::emit();
+#endif
+        __syncthreads();
+    }
 
     __device__ __forceinline__ static void run(const Segment &sg, int64_t m, int64_t n, int64_t m0, int64_t n0,
-                                               int64_t tbeg, int64_t tend, f32x4 (&acc)[FM][FN], uint4 *lds,
-                                               const float *lcode, const float *lcode2, int tid, int wm0,
-                                               int wn0) {
+                                               int64_t tbeg, int64_t tend, f32x4 (&acc)[FM][FN], uint4 *lds0,
+                                               uint4 *lds1, const float *lcode, const float *lcode2, int tid,
+                                               int wm0, int wn0) {
         if (tbeg >= tend) return;
         const int lane = tid & 63;
-        Fast<SA, BM, 1, THREADS> la;
-        Fast<SB, BN, FN, THREADS> lb;
+        LA la;
+        LB lb;
         la.init(sg.a, m, sg.k, m0, tid);
         lb.init(sg.b, n, sg.k, n0, tid);
         const float off_a = is_nf4<SA>() ? *sg.a.offset : 0.f;
         const float off_b = is_nf4<SB>() ? *sg.b.offset : 0.f;
         __syncthreads();  // every wave is done with the buffers of a previous segment
-        la.issue(lds, tbeg * kBK);
-        lb.issue(lds + BM * 8, tbeg * kBK);
-        la.commit(lds, lcode, lcode2, off_a);
-        lb.commit(lds + BM * 8, lcode, lcode2, off_b);
-        __builtin_amdgcn_s_waitcnt(0);  // LDS-DMA writes complete before the barrier publishes them
+        la.issue(lds0, tbeg * kBK);
+        lb.issue(lds0 + BM * 8, tbeg * kBK);
+        la.commit(lds0, lcode, lcode2, off_a);
+        lb.commit(lds0 + BM * 8, lcode, lcode2, off_b);
+        la.issue(lds1, (tbeg + 1) * kBK);
+        lb.issue(lds1 + BM * 8, (tbeg + 1) * kBK);
         __syncthreads();
-        for (int64_t t = tbeg; t < tend; ++t) {
-            uint4 *cur = lds + ((t - tbeg) & 1) * kStage;
-            uint4 *nxt = lds + (((t - tbeg) & 1) ^ 1) * kStage;
-            // Tile t+1 (past the end: masked to zeros, never consumed) into the other stage,
-            // which every wave finished reading before the previous barrier.
-            la.issue(nxt, (t + 1) * kBK);
-            lb.issue(nxt + BM * 8, (t + 1) * kBK);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int ks = 0; ks < kBK / 32; ++ks) {
-                const int chunk = ks * 4 + (lane >> 4);
-                uint4 af[FM], bf[FN];
-#pragma unroll
-                for (int i = 0; i < FM; ++i) af[i] = cur[slot<1>(wm0 + i * 16 + (lane & 15), chunk)];
-#pragma unroll
-                for (int j = 0; j < FN; ++j) bf[j] = cur[BM * 8 + slot<FN>(wn0 + (lane & 15) * FN + j, chunk)];
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
-            }
-#ifndef CT_INTERLEAVE_COMMIT
-            __builtin_amdgcn_sched_barrier(0);
-#endif
-            la.commit(nxt, lcode, lcode2, off_a);
-            lb.commit(nxt + BM * 8, lcode, lcode2, off_b);
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
+        // Step t reads stage (t - tbeg) % 2, which holds tile t; the registers hold tile t+1.
+        // Tiles past the end are masked to zeros and never consumed.
+        int64_t t = tbeg;
+        for (; t + 1 < tend; t += 2) {
+            step(la, lb, lds0, lds1, (t + 2) * kBK, acc, lcode, lcode2, off_a, off_b, lane, wm0, wn0);
+            step(la, lb, lds1, lds0, (t + 3) * kBK, acc, lcode, lcode2, off_a, off_b, lane, wm0, wn0);
         }
+        if (t < tend) step(la, lb, lds0, lds1, (t + 2) * kBK, acc, lcode, lcode2, off_a, off_b, lane, wm0, wn0);
     }
 };
 
@@ -613,7 +658,8 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     constexpr int FM = WM / 16, FN = WN / 16;
     static_assert(MODE == 2 || (WAVES_M == 2 && WAVES_N == 2), "the generic runner uses 4 waves");
     constexpr bool kNF4 = is_nf4<A0>() || is_nf4<B0>() || is_nf4<A1>() || is_nf4<B1>();
-    __shared__ uint4 lds[2 * (BM + BN) * 8];
+    __shared__ uint4 lds0[(BM + BN) * 8];
+    __shared__ uint4 lds1[(BM + BN) * 8];
     __shared__ float lcode[kNF4 ? 16 : 1];
     __shared__ float lcode2[kNF4 ? 256 : 1];
 
@@ -654,20 +700,20 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     {
         const int64_t b = tbeg, e = tend < t0 ? tend : t0;
         if constexpr (MODE == 2)
-            FastRunner<BM, BN, A0, B0, WAVES_M, WAVES_N>::run(p.seg[0], p.m, p.n, m0, n0, b, e, acc, lds, lcode, lcode2, tid, wm0,
-                                            wn0);
+            FastRunner<BM, BN, A0, B0, WAVES_M, WAVES_N>::run(p.seg[0], p.m, p.n, m0, n0, b, e, acc, lds0, lds1,
+                                                              lcode, lcode2, tid, wm0, wn0);
         else
-            SegmentRunner<BM, BN, A0, B0, VEC>::run(p.seg[0], p.m, p.n, m0, n0, b, e, acc, lds, lcode, lcode2,
-                                                    tid, wm0, wn0);
+            SegmentRunner<BM, BN, A0, B0, VEC>::run(p.seg[0], p.m, p.n, m0, n0, b, e, acc, lds0, lds1, lcode,
+                                                    lcode2, tid, wm0, wn0);
     }
     if (t1 > 0) {
         const int64_t b = tbeg > t0 ? tbeg - t0 : 0, e = tend - t0;
         if constexpr (MODE == 2)
-            FastRunner<BM, BN, A1, B1, WAVES_M, WAVES_N>::run(p.seg[1], p.m, p.n, m0, n0, b, e, acc, lds, lcode, lcode2, tid, wm0,
-                                            wn0);
+            FastRunner<BM, BN, A1, B1, WAVES_M, WAVES_N>::run(p.seg[1], p.m, p.n, m0, n0, b, e, acc, lds0, lds1,
+                                                              lcode, lcode2, tid, wm0, wn0);
         else
-            SegmentRunner<BM, BN, A1, B1, VEC>::run(p.seg[1], p.m, p.n, m0, n0, b, e, acc, lds, lcode, lcode2,
-                                                    tid, wm0, wn0);
+            SegmentRunner<BM, BN, A1, B1, VEC>::run(p.seg[1], p.m, p.n, m0, n0, b, e, acc, lds0, lds1, lcode,
+                                                    lcode2, tid, wm0, wn0);
     }
 
     // ------------------------------------------------------------------ epilogue
@@ -1043,7 +1089,7 @@ bool nf4_fusable(const ct_nf4_weight *w) {
 
 using namespace ct;
 
-extern "C" int ct_abi_version(void) { return 2; }
+extern "C" int ct_abi_version(void) { return 3; }
 
 extern "C" const char *ct_status_string(int status) {
     switch (status) {
@@ -1098,12 +1144,38 @@ extern "C" int ct_gemm(const void *a, int64_t lda, int32_t trans_a, const void *
     return to_status(run(pr, stream));
 }
 
-extern "C" int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, int64_t r) {
+namespace ct {
+namespace {
+#ifndef CT_MATERIALIZE_ROWS
+#define CT_MATERIALIZE_ROWS 512
+#endif
+// An NF4 base weight is decoded inside the GEMM's operand loader only while the rows are
+// few: each 256-row tile decodes its slice of the weight again, and from kMaterializeRows
+// rows on one ct_nf4_dequant pass into the workspace (the reference's materialize) plus
+// the dense GEMM is faster. Both give identical results.
+constexpr int64_t kMaterializeRows = CT_MATERIALIZE_ROWS;
+bool materialize_nf4(const ct_nf4_weight *w, int64_t m) { return w && m >= kMaterializeRows; }
+int64_t weight_bytes(int64_t n, int64_t k) { return (n * k * 2 + 255) & ~int64_t{255}; }
+
+// Splits the workspace into the materialized bf16 weight and the remainder.
+int take_weight(void *&workspace, int64_t &workspace_bytes, int64_t n, int64_t k, void *&wbuf) {
+    const int64_t need = weight_bytes(n, k);
+    if (!workspace || workspace_bytes < need) return -CT_EINVAL_WORKSPACE;
+    wbuf = workspace;
+    workspace = static_cast<char *>(workspace) + need;
+    workspace_bytes -= need;
+    return 0;
+}
+}  // namespace
+}  // namespace ct
+
+extern "C" int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, int64_t r, int32_t nf4) {
     const int64_t inner = ct_gemm_workspace(m, r, k, 0, 1, CT_BF16);
     const int64_t ks[2] = {k, r};
     const int sb[2] = {SRC_NF4, SRC_KC};  // the dense weight (KC) has the same split shape
     const int64_t main = problem_workspace(m, n, ks, r > 0 ? 2 : 1, sb);
-    return inner > main ? inner : main;  // the two launches run in order on one stream
+    const int64_t rest = inner > main ? inner : main;  // the two launches run in order on one stream
+    return (nf4 && m >= kMaterializeRows) ? weight_bytes(n, k) + rest : rest;
 }
 
 extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense, const ct_nf4_weight *w_nf4,
@@ -1118,7 +1190,17 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
         const int st = validate_nf4(w_nf4);
         if (st) return st;
         if (w_nf4->rows != n || w_nf4->cols != k) return -CT_EINVAL_SHAPE;
-        if (!nf4_fusable(w_nf4)) return -CT_EINVAL_LAYOUT;
+        if (materialize_nf4(w_nf4, m)) {
+            void *wbuf = nullptr;
+            const int ws = take_weight(workspace, workspace_bytes, n, k, wbuf);
+            if (ws) return ws;
+            const int dq = ct_nf4_dequant(w_nf4, wbuf, CT_BF16, stream);
+            if (dq) return dq;
+            w_dense = wbuf;
+            w_nf4 = nullptr;
+        } else if (!nf4_fusable(w_nf4)) {
+            return -CT_EINVAL_LAYOUT;
+        }
     }
     if (r > 0) {
         // xa = x a^T  (NT, bf16 out)
@@ -1160,12 +1242,13 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
     return to_status(e);
 }
 
-extern "C" int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, int64_t r) {
+extern "C" int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, int64_t r, int32_t nf4) {
     const int64_t inner = ct_gemm_workspace(m, r, n, 0, 0, CT_BF16);
     const int64_t ks[2] = {n, r};
     const int sb[2] = {SRC_NF4T, SRC_KS};
     const int64_t main = problem_workspace(m, k, ks, r > 0 ? 2 : 1, sb);
-    return inner > main ? inner : main;
+    const int64_t rest = inner > main ? inner : main;
+    return (nf4 && m >= kMaterializeRows) ? weight_bytes(n, k) + rest : rest;
 }
 
 extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_dense, const ct_nf4_weight *w_nf4,
@@ -1180,7 +1263,17 @@ extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_den
         const int st = validate_nf4(w_nf4);
         if (st) return st;
         if (w_nf4->rows != n || w_nf4->cols != k) return -CT_EINVAL_SHAPE;
-        if (!nf4_fusable(w_nf4)) return -CT_EINVAL_LAYOUT;
+        if (materialize_nf4(w_nf4, m)) {
+            void *wbuf = nullptr;
+            const int ws = take_weight(workspace, workspace_bytes, n, k, wbuf);
+            if (ws) return ws;
+            const int dq = ct_nf4_dequant(w_nf4, wbuf, CT_BF16, stream);
+            if (dq) return dq;
+            w_dense = wbuf;
+            w_nf4 = nullptr;
+        } else if (!nf4_fusable(w_nf4)) {
+            return -CT_EINVAL_LAYOUT;
+        }
     }
     if (r > 0) {
         // low = dy b  (NN, bf16 out)

@@ -42,14 +42,46 @@ struct GemmParams {
 // ------------------------------------------------------------------ LDS layout and NF4 decode
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0, 0, 0, 0); }
 
-// LDS slot of chunk `chunk` (0..7) of tile row `row`; SWZ_DIV rows share a swizzle value.
-// With v = row / SWZ_DIV the 16-byte chunk moves to position chunk ^ ((v ^ v / 8) % 8):
-// the 16 rows of an MFMA fragment read (consecutive v) land on distinct positions in each
-// half, and so do the rows 8 apart that the transposing loaders write together.
-template <int SWZ_DIV>
+// LDS slot (16-byte unit) of chunk `chunk` (0..7) of LDS row `row`. Rows are 128 bytes,
+// so a 256-byte line of 16 units holds rows 2L and 2L+1; inside line L the unit index
+// (row & 1) * 8 + chunk is XORed with line_swizzle(L) = 2 (L mod 8).
+//
+// gfx950 serves a ds_read_b128 in four groups of 16 lanes, {0-7, 24-31}, {8-15, 16-23},
+// {32-39, 56-63} and {40-47, 48-55}, over 64 four-byte banks, i.e. the 16 units of a
+// 256-byte line (measured on MI355X with exec-masked probes: bank = unit mod 16, no
+// address hash). A group is conflict-free when its 16 lanes hit 16 distinct units mod 16.
+// Every MFMA fragment read takes LDS rows R0 + (l mod 16), R0 a multiple of 16, at chunk
+// 4 ks + l / 16; with this swizzle all of them are conflict-free, and since the swizzle
+// depends only on l, the fragments of one lane differ by immediate offsets. (A per-row
+// XOR of the chunk alone leaves these reads two-way conflicted, halving LDS throughput.)
+__device__ __forceinline__ int line_swizzle(int line) { return (line & 7) << 1; }
 __device__ __forceinline__ int slot(int row, int chunk) {
-    const int v = row / SWZ_DIV;
-    return row * 8 + (chunk ^ ((v ^ (v >> 3)) & 7));
+    const int line = row >> 1;
+    return (line << 4) + ((((row & 1) << 3) | chunk) ^ line_swizzle(line));
+}
+// Inverse of slot(): the LDS row and chunk stored in unit `s`.
+__device__ __forceinline__ void slot_coords(int s, int &row, int &chunk) {
+    const int line = s >> 4;
+    const int w = (s & 15) ^ line_swizzle(line);
+    row = (line << 1) | (w >> 3);
+    chunk = w & 7;
+}
+// LDS row of tile row n for a side whose MFMA fragments give each lane FRAG consecutive
+// output columns (lane m of a 16 x (16 FRAG) wave tile holds columns FRAG m .. FRAG m +
+// FRAG - 1, so its epilogue stores are contiguous): column FRAG m + j goes to LDS row
+// 16 j + m of the wave's block, so fragment j reads 16 consecutive LDS rows. FRAG = 1 is
+// the identity.
+template <int FRAG>
+__device__ __forceinline__ int frag_row(int n) {
+    if constexpr (FRAG == 1) return n;
+    constexpr int W = 16 * FRAG;
+    return (n & ~(W - 1)) | ((n % FRAG) << 4) | ((n % W) / FRAG);
+}
+template <int FRAG>
+__device__ __forceinline__ int frag_row_inv(int s) {
+    if constexpr (FRAG == 1) return s;
+    constexpr int W = 16 * FRAG;
+    return (s & ~(W - 1)) | ((s & 15) * FRAG) | ((s % W) >> 4);
 }
 
 // Eight nibbles of one packed dword -> eight bf16 (element 2j from the high nibble of byte j).
@@ -67,7 +99,6 @@ __device__ __forceinline__ uint4 nf4_decode8(uint32_t d, float s, const float *l
 // ------------------------------------------------------------------ buffer loads
 // Raw buffer loads: the hardware range check returns zeros past num_records, and an
 // invalid lane is pointed past the range, so loops over k need no branches.
-typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr uint32_t kOOB = 0x80000000u;  // a byte offset beyond every buffer range used here
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int64_t bytes) {

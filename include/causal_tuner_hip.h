@@ -125,13 +125,15 @@ int ct_nf4_fused_supported(const ct_nf4_weight *w);
  *   out = bf16(x w^T + bias + xa b^T)               [m, n]
  * with the base GEMM and the rank-r epilogue as one contraction over k + r columns.
  * Exactly one of w_dense (bf16 [n, k]) or w_nf4 (rows n, cols k) is non-null. With w_nf4
- * the weight is decoded tile by tile into LDS inside the GEMM (materialize fused away),
- * bit-identical to ct_nf4_dequant's bf16 output; returns -CT_EINVAL_LAYOUT when
- * ct_nf4_fused_supported(w_nf4) is 0.
+ * and m >= 512 the weight is first decoded by ct_nf4_dequant into bf16 inside the
+ * workspace (the reference's materialize) and the dense GEMM follows; below that the
+ * weight is decoded tile by tile into LDS inside the GEMM (materialize fused away, which
+ * needs ct_nf4_fused_supported(w_nf4), else -CT_EINVAL_LAYOUT). Both paths give results
+ * bit-identical to ct_nf4_dequant's bf16 weight in the dense GEMM.
  * x [m, k] (ldx), a bf16 [r, k], b bf16 [n, r], bias bf16 [n] or null, out [m, n] (ldo),
- * xa bf16 [m, r] contiguous.
+ * xa bf16 [m, r] contiguous. The workspace query takes nf4 = 1 for an NF4 weight.
  */
-int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, int64_t r);
+int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, int64_t r, int32_t nf4);
 int ct_forward_linear(const void *x, int64_t ldx,
                       const void *w_dense, const ct_nf4_weight *w_nf4,
                       const void *a, const void *b, const void *bias,
@@ -143,11 +145,11 @@ int ct_forward_linear(const void *x, int64_t ldx,
  * Replaces input_gradient (kernels/linear.py:36-39):
  *   low = bf16(dy b)                                 [m, r]   (written)
  *   dx  = bf16(dy w + low a (+ dx if add))           [m, k]
- * dy [m, n] (lddy), w as in ct_forward_linear (an NF4 weight is decoded into LDS in the
- * transposed layout this product needs), a bf16 [r, k], b bf16 [n, r], dx [m, k] (lddx),
- * low bf16 [m, r] contiguous.
+ * dy [m, n] (lddy), w as in ct_forward_linear (a fused NF4 weight is decoded into LDS in
+ * the transposed layout this product needs), a bf16 [r, k], b bf16 [n, r], dx [m, k]
+ * (lddx), low bf16 [m, r] contiguous.
  */
-int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, int64_t r);
+int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, int64_t r, int32_t nf4);
 int ct_input_gradient(const void *dy, int64_t lddy,
                       const void *w_dense, const ct_nf4_weight *w_nf4,
                       const void *a, const void *b,

@@ -43,7 +43,7 @@ def test_library_embeds_gfx950_code_objects():
 
 def test_status_strings_and_version():
     lib = _native.library()
-    assert lib.ct_abi_version() == 2
+    assert lib.ct_abi_version() == 3
     assert lib.ct_status_string(0) == b"success"
     assert b"workspace" in lib.ct_status_string(-5)
     assert b"fused" in lib.ct_status_string(-6)
@@ -85,8 +85,12 @@ def test_host_side_argument_errors_return_negative_status():
     assert lib.ct_gemm_workspace(16, 256, 6144, 0, 1, _native.CT_BF16) > 0
     assert lib.ct_gemm_workspace(8192, 256, 4096, 0, 1, _native.CT_BF16) == 0
     assert lib.ct_gemm_workspace(16, 256, 6144, 0, 1, _native.CT_F32) == 0
-    assert lib.ct_input_gradient_workspace(16, 24576, 6144, 256) > 0
-    assert lib.ct_forward_linear_workspace(8192, 4096, 4096, 256) == 0
+    assert lib.ct_input_gradient_workspace(16, 24576, 6144, 256, 1) > 0
+    assert lib.ct_forward_linear_workspace(8192, 4096, 4096, 256, 0) == 0
+    # many rows: an NF4 weight is materialized as bf16 inside the workspace first
+    assert lib.ct_forward_linear_workspace(8192, 4096, 4096, 256, 1) >= 4096 * 4096 * 2
+    assert lib.ct_input_gradient_workspace(8192, 11008, 4096, 256, 1) >= 11008 * 4096 * 2
+    assert lib.ct_forward_linear_workspace(64, 4096, 4096, 256, 1) < 4096 * 4096 * 2
     # workspace too small for a split reduction
     need = lib.ct_accumulate_workspace(256, 4096, 8192)
     assert need > 0

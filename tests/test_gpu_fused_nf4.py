@@ -1,7 +1,8 @@
 """Fused NF4 operands of the projection GEMMs (forward x w^T and the transposed dx = dy w).
 
 The fused loaders decode the packed weight tile by tile into LDS with the reference's
-decoding rule (kernels/nf4_cuda.py:16-29), so a projection over the packed weight must be
+decoding rule (kernels/nf4_cuda.py:16-29), and from 512 rows on the entry points decode it
+once into the workspace instead; either way a projection over the packed weight must be
 bit-identical to the same projection over the weight that `materialize` produces
 (kernels/linear.py:6-13): both run the same tile shape and summation order. The float64
 oracle bounds the result itself."""
@@ -17,8 +18,10 @@ from oracle import lora as olora
 pytestmark = pytest.mark.gpu
 
 # (m, k, n, r): tails in every dimension, odd ranks, and 256x256-tile shapes; m <= 64 runs
-# the few-row kernels (1, 2 and 4 row blocks; 1, 2 and 4 column blocks per workgroup).
+# the few-row kernels (1, 2 and 4 row blocks; 1, 2 and 4 column blocks per workgroup), and
+# from m = 512 on the entry points decode the weight into the workspace first.
 SHAPES = [(37, 96, 80, 8), (300, 256, 192, 5), (1, 64, 64, 4), (513, 1024, 1032, 16), (4096, 4096, 4096, 256),
+          (448, 4096, 4096, 64), (511, 1024, 2056, 16),
           (2048, 4096, 11008, 256), (4096, 11008, 4096, 64), (16, 6144, 24576, 256), (64, 24576, 6144, 256),
           (5, 1024, 512, 8), (29, 2048, 16384, 16), (64, 4096, 8192, 128), (3, 128, 8200, 4)]
 
