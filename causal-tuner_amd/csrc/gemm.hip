@@ -373,6 +373,10 @@ __device__ __forceinline__ void store_part(uint4 *stage, int byte, const uint32_
 
 // KS: 8x8 blocks (8 reduction rows x 8 output rows), split over LPB lanes that take
 // R = 8 / LPB reduction rows each; transposed in registers, R values per LDS write.
+// Adjacent lanes take the parts of one block, the next lanes its neighbours along the
+// reduction (the 8 chunks of one LDS row), then the next 8 output rows: each store
+// instruction then fills whole 256-byte lines instead of piling 16 lanes onto the same
+// banks (rows 8 apart share a swizzle position).
 template <int ROWS, int FRAG, int THREADS>
 struct Fast<SRC_KS, ROWS, FRAG, THREADS> {
     static constexpr int kLPB = THREADS / ROWS;
@@ -385,10 +389,10 @@ struct Fast<SRC_KS, ROWS, FRAG, THREADS> {
     bool valid;
     uint4 v[R];
     __device__ __forceinline__ void init(const Operand &o, int64_t rows, int64_t kext, int64_t r0, int tid) {
-        const int b = tid % ROWS;
-        h = tid / ROWS;
-        col = (b % (ROWS / 8)) * 8;
-        chunk = b / (ROWS / 8);
+        const int b = tid / kLPB;
+        h = tid % kLPB;
+        col = (b >> 3) * 8;
+        chunk = b & 7;
         const uint16_t *p = static_cast<const uint16_t *>(o.p) + r0;
         r = make_rsrc(p, kext > 0 ? ((kext - 1) * o.ld + (rows - r0)) * 2 : 0);
         valid = r0 + col < rows;
@@ -475,7 +479,6 @@ struct Fast<SRC_NF4, ROWS, FRAG, THREADS> {
 // split over LPB lanes that take R = 8 / LPB weight rows each.
 template <int ROWS, int FRAG, int THREADS>
 struct Fast<SRC_NF4T, ROWS, FRAG, THREADS> {
-    static constexpr int kCB = ROWS / 8;
     static constexpr int kLPB = THREADS / ROWS;
     static constexpr int R = 8 / kLPB;
     static constexpr int kVmem = 3 * R, kWrites = 8;
@@ -499,10 +502,10 @@ struct Fast<SRC_NF4T, ROWS, FRAG, THREADS> {
         const int64_t nb = (n + (int64_t{1} << lb) - 1) >> lb;
         ra = make_rsrc(o.absmax, nb);
         r2 = make_rsrc(o.absmax2, ((nb + (int64_t{1} << lb2) - 1) >> lb2) * 4);
-        const int b = tid % ROWS;
-        h = tid / ROWS;
-        col = (b % kCB) * 8;
-        chunk = b / kCB;
+        const int b = tid / kLPB;  // lane order as in the KS loader
+        h = tid % kLPB;
+        col = (b >> 3) * 8;
+        chunk = b & 7;
         row0 = chunk * 8 + h * R;
         colok = r0 + col < rows;
         ld = (uint32_t)o.ld;
@@ -679,7 +682,15 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     const int gsize = p.tiles_m - first_m < kGroupM ? p.tiles_m - first_m : kGroupM;
     const int tm = first_m + (rid % (kGroupM * p.tiles_n)) % gsize;
     const int tn = (rid % (kGroupM * p.tiles_n)) / gsize;
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t m0 = (int64_t)tm * BM;
+    // Grouped products: the tile's operands, its column offset inside them and its column
+    // count; `out_shift` moves its output columns past group 0.
+    constexpr bool kGrouped = OUT == CT_F32 && A0 == SRC_KS && B0 == SRC_KS;  // the parameter gradients
+    const bool second = kGrouped && p.group_tiles > 0 && tn >= p.group_tiles;
+    const Segment &sg0 = second ? p.seg[1] : p.seg[0];
+    const int64_t n0 = (int64_t)(second ? tn - p.group_tiles : tn) * BN;
+    const int64_t ncols = second ? p.n1 : p.n;
+    const int64_t out_shift = second ? (int64_t)p.group_tiles * BN : 0;
 
     if constexpr (kNF4) {
         if (tid < 16) lcode[tid] = p.code[tid];
@@ -693,17 +704,17 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int64_t t0 = cdiv(p.seg[0].k, kBK);
+    const int64_t t0 = cdiv(sg0.k, kBK);
     const int64_t t1 = p.nseg > 1 ? cdiv(p.seg[1].k, kBK) : 0;
     const int64_t tbeg = (int64_t)blockIdx.z * p.tiles_per_split;
     const int64_t tend = tbeg + p.tiles_per_split < t0 + t1 ? tbeg + p.tiles_per_split : t0 + t1;
     {
         const int64_t b = tbeg, e = tend < t0 ? tend : t0;
         if constexpr (MODE == 2)
-            FastRunner<BM, BN, A0, B0, WAVES_M, WAVES_N>::run(p.seg[0], p.m, p.n, m0, n0, b, e, acc, lds0, lds1,
+            FastRunner<BM, BN, A0, B0, WAVES_M, WAVES_N>::run(sg0, p.m, ncols, m0, n0, b, e, acc, lds0, lds1,
                                                               lcode, lcode2, tid, wm0, wn0);
         else
-            SegmentRunner<BM, BN, A0, B0, VEC>::run(p.seg[0], p.m, p.n, m0, n0, b, e, acc, lds0, lds1, lcode,
+            SegmentRunner<BM, BN, A0, B0, VEC>::run(sg0, p.m, ncols, m0, n0, b, e, acc, lds0, lds1, lcode,
                                                     lcode2, tid, wm0, wn0);
     }
     if (t1 > 0) {
@@ -721,8 +732,8 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     const int64_t col = n0 + wn0 + (lane & 15) * FN;
     float bias[FN];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) bias[j] = (p.bias && col + j < p.n) ? bf16_to_f32(p.bias[col + j]) : 0.f;
-    const bool full = col + FN <= p.n;
+    for (int j = 0; j < FN; ++j) bias[j] = (p.bias && col + j < ncols) ? bf16_to_f32(p.bias[col + j]) : 0.f;
+    const bool full = col + FN <= ncols;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -733,7 +744,8 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) v[j] = acc[i][j][e] + bias[j];
             if constexpr (OUT == CT_F32) {
-                float *c = static_cast<float *>(p.c) + (int64_t)blockIdx.z * p.split_stride + row * p.ldc + col;
+                float *c = static_cast<float *>(p.c) + (int64_t)blockIdx.z * p.split_stride + row * p.ldc +
+                           out_shift + col;
                 if (VEC && full && FN % 4 == 0) {
 #pragma unroll
                     for (int j = 0; j < FN; j += 4) {
@@ -744,16 +756,16 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
                 } else {
 #pragma unroll
                     for (int j = 0; j < FN; ++j) {
-                        if (!full && col + j >= p.n) break;
+                        if (!full && col + j >= ncols) break;
                         c[j] = p.beta ? v[j] + c[j] : v[j];
                     }
                 }
             } else {
-                uint16_t *c = static_cast<uint16_t *>(p.c) + row * p.ldc + col;
+                uint16_t *c = static_cast<uint16_t *>(p.c) + row * p.ldc + out_shift + col;
                 if (p.beta) {
 #pragma unroll
                     for (int j = 0; j < FN; ++j)
-                        if (full || col + j < p.n) v[j] = v[j] + bf16_to_f32(c[j]);
+                        if (full || col + j < ncols) v[j] = v[j] + bf16_to_f32(c[j]);
                 }
                 if (VEC && full && FN >= 2) {
                     uint32_t w[FN / 2];
@@ -765,7 +777,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
                 } else {
 #pragma unroll
                     for (int j = 0; j < FN; ++j) {
-                        if (!full && col + j >= p.n) break;
+                        if (!full && col + j >= ncols) break;
                         c[j] = bf16_bits(v[j]);
                     }
                 }
@@ -813,6 +825,34 @@ __global__ __launch_bounds__(256) void reduce_splits(const float *__restrict__ w
     }
 }
 
+// A fill kernel rather than hipMemsetAsync, so the call stays safe inside graph capture.
+__global__ __launch_bounds__(256) void fill_zero(float *p, int64_t count) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < count) p[i] = 0.f;
+}
+
+// Sums the split partials of the grouped parameter-gradient GEMM, ws[z][i][c] with
+// c < width, in split order: columns below `gcols` are da[i][c] (c < k), the rest are
+// db[c - gcols][i] (< n), i.e. dB^T is written transposed.
+__global__ __launch_bounds__(256) void reduce_param(const float *__restrict__ ws, int splits, int64_t stride,
+                                                    int64_t r, int64_t width, int64_t gcols, int64_t k,
+                                                    int64_t n, float *da, float *db, int add) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= r * width) return;
+    const int64_t i = idx / width, c = idx % width;
+    float *o;
+    if (c < gcols) {
+        if (c >= k) return;
+        o = da + i * k + c;
+    } else {
+        if (c - gcols >= n) return;
+        o = db + (c - gcols) * r + i;
+    }
+    float s = ws[idx];
+    for (int z = 1; z < splits; ++z) s += ws[z * stride + idx];
+    *o = add ? s + *o : s;
+}
+
 // ------------------------------------------------------------------------ host side
 enum Tile { TILE_256 = 0, TILE_128 = 1, TILE_64 = 2 };
 constexpr int kTileEdge[3] = {256, 128, 64};
@@ -838,16 +878,21 @@ constexpr bool is_nf4_host(int src) { return src == SRC_NF4 || src == SRC_NF4T; 
 
 // Vector (16-byte) operand access needs aligned bases, leading dimensions that are
 // multiples of 8 elements, and 8-multiple extents along each contiguous dimension.
+// Segments the kernels read: both for a two-segment contraction or a grouped launch.
+int operand_segments(const GemmParams &p) { return p.group_tiles > 0 ? 2 : p.nseg; }
+// Columns of segment s's B operand.
+int64_t segment_cols(const GemmParams &p, int s) { return (p.group_tiles > 0 && s == 1) ? p.n1 : p.n; }
+
 bool vec_ok(const Problem &pr) {
     const GemmParams &p = pr.p;
-    for (int s = 0; s < p.nseg; ++s) {
+    for (int s = 0; s < operand_segments(p); ++s) {
         const Segment &g = p.seg[s];
         const int sa = pr.src[2 * s], sb = pr.src[2 * s + 1];
         if (g.k % 8) return false;
         if (!is_nf4_host(sa) && (!aligned16(g.a.p) || g.a.ld % 8)) return false;
         if (!is_nf4_host(sb) && (!aligned16(g.b.p) || g.b.ld % 8)) return false;
         if (sa == SRC_KS && p.m % 8) return false;
-        if (sb == SRC_KS && p.n % 8) return false;
+        if (sb == SRC_KS && segment_cols(p, s) % 8) return false;
     }
     if (!aligned16(p.c) || p.ldc % 8) return false;
     return true;
@@ -858,11 +903,11 @@ bool fast_ok(const Problem &pr) {
     if (!pr.vec) return false;
     const GemmParams &p = pr.p;
     constexpr int64_t kLimit = int64_t{1} << 31;
-    for (int s = 0; s < p.nseg; ++s) {
+    for (int s = 0; s < operand_segments(p); ++s) {
         const Segment &g = p.seg[s];
         const int src[2] = {pr.src[2 * s], pr.src[2 * s + 1]};
         const Operand *op[2] = {&g.a, &g.b};
-        const int64_t rows[2] = {p.m, p.n};
+        const int64_t rows[2] = {p.m, segment_cols(p, s)};
         for (int i = 0; i < 2; ++i) {
             if (is_nf4_host(src[i])) {
                 const int64_t n = (src[i] == SRC_NF4 ? rows[i] : g.k) * op[i]->ld;
@@ -889,7 +934,7 @@ hipError_t launch_cfg(const GemmParams &p0, int tile, int splits, hipStream_t s)
     GemmParams p = p0;
     const int e = kTileEdge[tile];
     p.tiles_m = (int)cdiv(p.m, e);
-    p.tiles_n = (int)cdiv(p.n, e);
+    p.tiles_n = (int)(p.group_tiles > 0 ? p.group_tiles + cdiv(p.n1, e) : cdiv(p.n, e));
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)splits);
     if (tile == TILE_256 && MODE == 2) gemm_big8<A0, B0, A1, B1, OUT><<<grid, dim3(512), 0, s>>>(p);
     else if (tile == TILE_256) gemm_big<A0, B0, A1, B1, MODE, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
@@ -1141,6 +1186,14 @@ extern "C" int ct_gemm(const void *a, int64_t lda, int32_t trans_a, const void *
     pr.ws = workspace;
     pr.ws_bytes = workspace ? workspace_bytes : 0;
     pr.vec = vec_ok(pr);
+#ifdef CT_TUNING
+    if (getenv("CT_GEMM_RED") && !bias && workspace) {
+        int status = 0;
+        const hipError_t e = run_reduction(pr, c, ldc, beta, workspace, workspace_bytes, stream, &status);
+        return status ? status : to_status(e);
+    }
+    if (const char *env = getenv("CT_TILE")) pr.tile = atoi(env);
+#endif
     return to_status(run(pr, stream));
 }
 
@@ -1345,11 +1398,38 @@ extern "C" int ct_accumulate(float *out, int64_t ldo, const void *left, int64_t 
     return st ? st : to_status(e);
 }
 
+namespace ct {
+namespace {
+// One launch computes dA = low^T x ([r, k]) and dB^T = xa^T dy ([r, n]) side by side: the
+// output is r rows by gt * e + n columns (gt column tiles for dA), the token reduction is
+// split so that the grid holds about one workgroup per CU, and reduce_param sums the
+// splits in order (bit-identical across calls) and writes dB transposed.
+struct ParamPlan {
+    int tile, splits, gt;
+    int64_t width;
+};
+ParamPlan param_plan(int64_t m, int64_t n, int64_t k, int64_t r) {
+    ParamPlan pl{};
+    pl.tile = r > 128 ? TILE_256 : (r > 64 ? TILE_128 : TILE_64);
+    const int64_t e = kTileEdge[pl.tile];
+    pl.gt = (int)cdiv(k, e);
+    pl.width = pl.gt * e + n;
+    const int64_t tiles = cdiv(r, e) * (pl.gt + cdiv(n, e));
+    const int64_t ktiles = cdiv(m, kBK);
+    int64_t s = cdiv(256, tiles > 0 ? tiles : 1);
+    const int64_t cap = ktiles / 8 > 1 ? ktiles / 8 : 1;
+    if (s > cap) s = cap;
+    if (s > 32) s = 32;
+    pl.splits = (int)(s < 1 ? 1 : s);
+    return pl;
+}
+int64_t param_workspace(const ParamPlan &pl, int64_t r) { return (int64_t)pl.splits * r * pl.width * 4; }
+}  // namespace
+}  // namespace ct
+
 extern "C" int64_t ct_parameter_gradients_workspace(int64_t m, int64_t n, int64_t k, int64_t r) {
-    if (m <= 0 || r <= 0) return 0;
-    const int64_t a = k > 0 ? split_workspace_bytes(r, k, m) : 0;
-    const int64_t b = n > 0 ? split_workspace_bytes(n, r, m) : 0;
-    return a > b ? a : b;  // dA and dB run in sequence on one stream and share the buffer
+    if (m <= 0 || r <= 0 || (n <= 0 && k <= 0)) return 0;
+    return param_workspace(param_plan(m, n, k, r), r);
 }
 
 extern "C" int ct_parameter_gradients(const void *x, int64_t ldx, const void *dy, int64_t lddy, const void *low,
@@ -1357,13 +1437,50 @@ extern "C" int ct_parameter_gradients(const void *x, int64_t ldx, const void *dy
                                       int64_t r, int32_t add, void *workspace, int64_t workspace_bytes,
                                       hipStream_t stream) {
     if (m < 0 || n < 0 || k < 0 || r < 0) return -CT_EINVAL_SHAPE;
-    if (r == 0) return 0;
-    if (!da || !db) return -CT_EINVAL_POINTER;
+    if (r == 0 || (n == 0 && k == 0)) return 0;
+    if ((k > 0 && !da) || (n > 0 && !db)) return -CT_EINVAL_POINTER;
+    if (m == 0) {  // empty reduction: zero gradients (or unchanged with add)
+        if (add) return 0;
+        if (k) fill_zero<<<(unsigned)cdiv(r * k, 256), 256, 0, stream>>>(da, r * k);
+        if (n) fill_zero<<<(unsigned)cdiv(n * r, 256), 256, 0, stream>>>(db, n * r);
+        return to_status(hipGetLastError());
+    }
+    if ((k > 0 && (!x || !low)) || (n > 0 && (!dy || !xa))) return -CT_EINVAL_POINTER;
+    if (ldx < k || lddy < n) return -CT_EINVAL_SHAPE;
+    const ParamPlan pl = param_plan(m, n, k, r);
+    if (!workspace || workspace_bytes < param_workspace(pl, r)) return -CT_EINVAL_WORKSPACE;
     const int slot = profile_open(CT_PROF_PARAM, stream);
-    // da[r, k] = low^T x : L(p=i, j=row) = low[row*r + i] -> trans_l; R(j=row, q) = x[row*ldx + q]
-    int st = ct_accumulate(da, k, low, r, 1, x, ldx, 0, r, k, m, add, workspace, workspace_bytes, stream);
-    // db[n, r] = dy^T xa : L(p=col, j=row) = dy[row*lddy + col] -> trans_l; R(j=row, q) = xa[row*r + q]
-    if (!st) st = ct_accumulate(db, r, dy, lddy, 1, xa, r, 0, n, r, m, add, workspace, workspace_bytes, stream);
+    Problem pr{};
+    // Group 0 (dA): A(i, t) = low[t][i], B(q, t) = x[t][q]; group 1 (dB^T): xa and dy.
+    Segment dA{dense(low, r), dense(x, ldx), m}, dB{dense(xa, r), dense(dy, lddy), m};
+    if (k > 0 && n > 0) {
+        pr.p.seg[0] = dA;
+        pr.p.seg[1] = dB;
+        pr.p.n = k;
+        pr.p.n1 = n;
+        pr.p.group_tiles = pl.gt;
+    } else {
+        pr.p.seg[0] = k > 0 ? dA : dB;
+        pr.p.n = k > 0 ? k : n;
+    }
+    pr.p.nseg = 1;
+    pr.p.m = r;
+    pr.p.c = workspace;
+    pr.p.ldc = pl.width;
+    pr.p.split_stride = r * pl.width;
+    pr.src[0] = pr.src[1] = pr.src[2] = pr.src[3] = SRC_KS;
+    pr.out = CT_F32;
+    pr.splits = pl.splits;
+    pr.tile = pl.tile;
+    pr.vec = vec_ok(pr);
+    hipError_t e = run(pr, stream);
+    if (e == hipSuccess) {
+        const int64_t gcols = k > 0 ? (int64_t)pl.gt * kTileEdge[pl.tile] : 0;
+        const unsigned grid = (unsigned)cdiv(r * pl.width, 256);
+        reduce_param<<<grid, 256, 0, stream>>>(static_cast<const float *>(workspace), pl.splits, r * pl.width, r,
+                                               pl.width, gcols, k, n, da, db, add);
+        e = hipGetLastError();
+    }
     profile_close(slot, stream, 2.0 * m * r * (double)(k + n));
-    return st;
+    return to_status(e);
 }

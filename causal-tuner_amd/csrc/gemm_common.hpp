@@ -37,6 +37,11 @@ struct GemmParams {
     const float *code;        // NF4 code book [16]
     const float *code2;       // NF4 second-level code book [256]
     float *split_ws;          // few-row kernels: fp32 split partials [splits][m][n]
+    // Grouped mode (group_tiles > 0, nseg == 1): column tiles tn >= group_tiles compute a
+    // second, independent product seg[1] with n1 columns, stored from output column
+    // group_tiles * BN on.
+    int group_tiles;
+    int64_t n1;
 };
 
 // ------------------------------------------------------------------ LDS layout and NF4 decode

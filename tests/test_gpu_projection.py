@@ -253,3 +253,34 @@ def test_c3_projection_against_fp32_torch_reference(name, k, n):
                              (grads[2], ref_db, "db")):
         norm = ((got.float() - want).norm() / want.norm()).item()
         assert norm <= 1e-3, (label, norm)
+
+
+@pytest.mark.parametrize("m,n,k,r", [(8192, 4096, 4096, 256), (2048, 128, 4096, 256), (4096, 11008, 4096, 256),
+                                     (300, 40, 72, 5), (777, 200, 136, 64), (520, 96, 0, 16), (520, 0, 96, 16)])
+def test_parameter_gradients_grouped_launch(m, n, k, r):
+    """dA = low^T x and dB = dy^T xa (kernels/linear.py:42-44) from one grouped launch with a
+    split token reduction: fp32 results against float64 on the host, NaN-filled outputs
+    ignored with add=False, add=True accumulates, and repeated calls are bit-identical."""
+    from causal_tuner.kernels.linear import parameter_gradients
+    g = torch.Generator(device="cuda").manual_seed(m + n + k + r)
+    x = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+    dy = torch.randn(m, n, device="cuda", generator=g).to(torch.bfloat16)
+    low = torch.randn(m, r, device="cuda", generator=g).to(torch.bfloat16)
+    xa = torch.randn(m, r, device="cuda", generator=g).to(torch.bfloat16)
+    da = torch.full((r, k), float("nan"), device="cuda")
+    db = torch.full((n, r), float("nan"), device="cuda")
+    parameter_gradients(x, dy, da, db, low, xa, add=False)
+    want_a = (low.double().T @ x.double()).cpu()
+    want_b = (dy.double().T @ xa.double()).cpu()
+    for got, want, name in ((da, want_a, "da"), (db, want_b, "db")):
+        if want.numel():
+            _, norm = olora.relative_error(got.cpu(), want)
+            assert norm <= 1e-5, (name, norm)
+    again_a, again_b = torch.empty_like(da), torch.empty_like(db)
+    parameter_gradients(x, dy, again_a, again_b, low, xa, add=False)
+    assert torch.equal(again_a, da) and torch.equal(again_b, db)
+    parameter_gradients(x, dy, again_a, again_b, low, xa, add=True)
+    for got, want, name in ((again_a, 2 * want_a, "da+"), (again_b, 2 * want_b, "db+")):
+        if want.numel():
+            _, norm = olora.relative_error(got.cpu(), want)
+            assert norm <= 1e-5, (name, norm)
