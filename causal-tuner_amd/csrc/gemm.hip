@@ -1040,8 +1040,8 @@ hipError_t run_reduction(Problem pr, void *out, int64_t ldo, int add, void *ws, 
                          hipStream_t s, int *status) {
     GemmParams &p = pr.p;
     const int64_t kred = p.seg[0].k;
-    int tile, splits;
-    choose_reduction(p.m, p.n, kred, &tile, &splits);
+    int tile = pr.tile, splits = pr.splits;
+    if (tile < 0 || splits < 1) choose_reduction(p.m, p.n, kred, &tile, &splits);
     *status = 0;
     pr.tile = tile;
     if (splits <= 1) {
@@ -1151,9 +1151,25 @@ extern "C" const char *ct_status_string(int status) {
 
 extern "C" int ct_nf4_fused_supported(const ct_nf4_weight *w) { return nf4_fusable(w) ? 1 : 0; }
 
+namespace ct {
+namespace {
+// Rank-r products (at most 256 columns, many rows, a long reduction): 128-wide tiles with
+// the reduction split 4 ways fill the GPU better than 64-wide tiles (measured on MI355X
+// at 8192 rows: 20-25% faster for reductions of 11008).
+bool lowrank_split(int64_t m, int64_t n, int64_t k, int *tile, int *splits) {
+    if (n > 256 || m < 4096 || k < 2048) return false;
+    *tile = TILE_128;
+    *splits = 4;
+    return true;
+}
+}  // namespace
+}  // namespace ct
+
 extern "C" int64_t ct_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t trans_a, int32_t trans_b,
                                      int32_t c_dtype) {
     if (trans_a || c_dtype != CT_BF16) return 0;
+    int tile, splits;
+    if (lowrank_split(m, n, k, &tile, &splits)) return (int64_t)splits * m * n * 4;
     const int64_t ks[2] = {k, 0};
     const int sb[2] = {trans_b ? SRC_KC : SRC_KS, trans_b ? SRC_KC : SRC_KS};
     return problem_workspace(m, n, ks, 1, sb);
@@ -1194,6 +1210,15 @@ extern "C" int ct_gemm(const void *a, int64_t lda, int32_t trans_a, const void *
     }
     if (const char *env = getenv("CT_TILE")) pr.tile = atoi(env);
 #endif
+    int tile, splits;
+    if (!bias && c_dtype == CT_BF16 && !trans_a && lowrank_split(m, n, k, &tile, &splits) && workspace &&
+        workspace_bytes >= (int64_t)splits * m * n * 4) {
+        pr.tile = tile;
+        pr.splits = splits;
+        int status = 0;
+        const hipError_t e = run_reduction(pr, c, ldc, beta, workspace, workspace_bytes, stream, &status);
+        return status ? status : to_status(e);
+    }
     return to_status(run(pr, stream));
 }
 
@@ -1416,11 +1441,25 @@ ParamPlan param_plan(int64_t m, int64_t n, int64_t k, int64_t r) {
     pl.width = pl.gt * e + n;
     const int64_t tiles = cdiv(r, e) * (pl.gt + cdiv(n, e));
     const int64_t ktiles = cdiv(m, kBK);
-    int64_t s = cdiv(256, tiles > 0 ? tiles : 1);
+    // At most 8 splits: beyond that the partial sums' traffic costs more than the extra
+    // workgroups gain (measured on MI355X at 8192 tokens).
+    int64_t s = 256 / (tiles > 0 ? tiles : 1);
     const int64_t cap = ktiles / 8 > 1 ? ktiles / 8 : 1;
     if (s > cap) s = cap;
-    if (s > 32) s = 32;
+    if (s > 8) s = 8;
     pl.splits = (int)(s < 1 ? 1 : s);
+#ifdef CT_TUNING
+    if (const char *env = getenv("CT_PARAM")) {
+        int t = 0, sp = 1;
+        if (sscanf(env, "%d,%d", &t, &sp) == 2) {
+            pl.tile = t;
+            const int64_t e2 = kTileEdge[t];
+            pl.gt = (int)cdiv(k, e2);
+            pl.width = pl.gt * e2 + n;
+            pl.splits = sp;
+        }
+    }
+#endif
     return pl;
 }
 int64_t param_workspace(const ParamPlan &pl, int64_t r) { return (int64_t)pl.splits * r * pl.width * 4; }

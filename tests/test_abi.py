@@ -81,12 +81,14 @@ def test_host_side_argument_errors_return_negative_status():
     assert lib.ct_gemm(16, 4, 0, 16, 4, 1, 16, 4, 9, null, 0, 4, 4, 4, null, 0, null) == -3
     # empty problems are no-ops
     assert lib.ct_gemm(null, 0, 0, null, 0, 1, null, 0, _native.CT_BF16, null, 0, 0, 0, 0, null, 0, null) == 0
-    # few-row problems ask for split workspace; large ones and fp32 outputs do not
+    # few-row problems and rank-r products over many rows ask for split workspace; large
+    # square ones and fp32 outputs do not
     assert lib.ct_gemm_workspace(16, 256, 6144, 0, 1, _native.CT_BF16) > 0
-    assert lib.ct_gemm_workspace(8192, 256, 4096, 0, 1, _native.CT_BF16) == 0
+    assert lib.ct_gemm_workspace(8192, 256, 4096, 0, 1, _native.CT_BF16) == 4 * 8192 * 256 * 4
+    assert lib.ct_gemm_workspace(8192, 4096, 4096, 0, 1, _native.CT_BF16) == 0
     assert lib.ct_gemm_workspace(16, 256, 6144, 0, 1, _native.CT_F32) == 0
     assert lib.ct_input_gradient_workspace(16, 24576, 6144, 256, 1) > 0
-    assert lib.ct_forward_linear_workspace(8192, 4096, 4096, 256, 0) == 0
+    assert lib.ct_forward_linear_workspace(8192, 4096, 4096, 256, 0) == 4 * 8192 * 256 * 4
     # many rows: an NF4 weight is materialized as bf16 inside the workspace first
     assert lib.ct_forward_linear_workspace(8192, 4096, 4096, 256, 1) >= 4096 * 4096 * 2
     assert lib.ct_input_gradient_workspace(8192, 11008, 4096, 256, 1) >= 11008 * 4096 * 2
