@@ -176,13 +176,17 @@ def cpu_baseline(budget_s=12.0):
 
 
 FAMILIES = {
-    "fwd_gemm": ("CT_PROF_FWD_GEMM", "fused projection GEMM of ct_forward_linear (x w^T + xa b^T, NF4 decoded in LDS)"),
-    "dx_gemm": ("CT_PROF_DX_GEMM", "fused projection GEMM of ct_input_gradient (dy w + low a, NF4 decoded in LDS)"),
-    "param": ("CT_PROF_PARAM", "ct_parameter_gradients (dA = low^T x, dB = dy^T xa, fp32)"),
+    "fwd_gemm": ("CT_PROF_FWD_GEMM", "projection GEMM of ct_forward_linear (x w^T + xa b^T + bias in one "
+                 "contraction; at 8192 rows the NF4 weight is first decoded by ct_nf4_dequant)"),
+    "dx_gemm": ("CT_PROF_DX_GEMM", "projection GEMM of ct_input_gradient (dy w + low a in one contraction; "
+                "NF4 weight decoded first as in the forward)"),
+    "param": ("CT_PROF_PARAM", "ct_parameter_gradients (dA = low^T x and dB^T = xa^T dy in one grouped launch, "
+              "fp32, plus the split reduction)"),
     "lowrank": ("CT_PROF_LOWRANK", "rank-r products inside the entry points (xa = x a^T, low = dy b)"),
+    "dequant": ("CT_PROF_DEQUANT", "in-step NF4 decode of the base weights (ct_nf4_dequant, bytes not flops)"),
 }
 # The dx family is one kernel instantiation for every C3 projection (all reach 256x256 tiles).
-KERNEL_NAMES = {"dx_gemm": "gemm_big8<KC, NF4T, KC, KS>", "fwd_gemm": "gemm_big8<KC, NF4, KC, KC> (q,o,gate,up,down) "
+KERNEL_NAMES = {"dx_gemm": "gemm_big8<KC, KS, KC, KS>", "fwd_gemm": "gemm_big8<KC, KC, KC, KC> (q,o,gate,up,down) "
                 "+ gemm_small<64,64,...> (k, v)"}
 
 
@@ -210,7 +214,7 @@ def pmc_summary(fetch_csv, write_csv, family, mib):
     """Per-launch HBM traffic of a kernel family from two rocprofv3 --pmc runs (FETCH_SIZE,
     WRITE_SIZE, KiB per dispatch), each scaled by the same counter's reading for the copy
     probe of `mib` MiB; written to profiles/<family>_traffic.json."""
-    patterns = {"dx_gemm": "gemm_big8<0, 3, 0, 1, 2>", "fwd_gemm": "gemm_big8<0, 2, 0, 0, 2>"}
+    patterns = {"dx_gemm": "gemm_big8<0, 1, 0, 1, 2>", "fwd_gemm": "gemm_big8<0, 0, 0, 0, 2>"}
     copy_bytes = mib << 20
 
     def read(path, counter):
@@ -286,13 +290,18 @@ def main():
             ms, launches, work = timer.read(getattr(_native, name))
             families[key] = {"what": what, "launches": launches, "total_ms": round(ms, 4),
                              "avg_us": round(ms * 1e3 / max(launches, 1), 2),
-                             "tflops": round(work / (ms * 1e-3) / 1e12, 2) if ms else None,
                              "share_of_step": round(ms / (elapsed * 1e3), 4)}
+            rate = work / (ms * 1e-3) if ms else None
+            if key == "dequant":
+                families[key]["GB/s"] = round(rate / 1e9, 1) if rate else None
+            else:
+                families[key]["tflops"] = round(rate / 1e12, 2) if rate else None
     ms_per_step = elapsed * 1e3 / args.steps
     tflops = step_flops() / (ms_per_step * 1e-3) / 1e12
     log(f"C3 step: {ms_per_step:.3f} ms, {tflops:.1f} TFLOP/s")
     for key, v in families.items():
-        log(f"  {key:9s} {v['launches']:4d} launches  avg {v['avg_us']:9.1f} us  {v['tflops']} TFLOP/s  "
+        rate = f"{v['GB/s']} GB/s" if "GB/s" in v else f"{v['tflops']} TFLOP/s"
+        log(f"  {key:9s} {v['launches']:4d} launches  avg {v['avg_us']:9.1f} us  {rate}  "
             f"{100 * v['share_of_step']:.1f}% of step")
     dominant = max(("fwd_gemm", "dx_gemm"), key=lambda k: families[k]["total_ms"])
     d = families[dominant]
