@@ -1,0 +1,77 @@
+"""Partial GPT-J rotary embedding on gfx950 (the rotary part of the reference's
+kernels/core_cuda.py).
+
+Same operator API as the reference: `rotate_owned_qk` (core_cuda.py:192-200) rotates the
+q and k outputs of a projection group in place, `inverse_rope_tile` (203-208) writes the
+inverse rotation of an upstream gradient tile into a private buffer, and `PartialRoPE`
+(211-229) is the autograd function behind `modeling.rotary.rotate`. All three run the HIP
+kernel `ct_rope` with the reference's rounding (each product rounded to the tensor type,
+then the sum or difference rounded again).
+"""
+
+import torch
+
+from . import _native
+
+
+def _rope(x, y, cosine, sine, head_dim, *, inverse, rotated_only):
+    """y <- RoPE(x) over [tokens, heads, head_dim] with cosine/sine [tokens, half]."""
+    if not (x.is_cuda and y.is_cuda and cosine.is_cuda and sine.is_cuda):
+        raise ValueError("RoPE kernels expect device tensors")
+    if not (x.is_contiguous() and y.is_contiguous() and cosine.is_contiguous() and sine.is_contiguous()):
+        raise ValueError("RoPE kernels expect contiguous tensors")
+    if x.dtype != y.dtype or cosine.dtype != sine.dtype:
+        raise ValueError("RoPE: mismatched element types")
+    if head_dim <= 0 or head_dim % 2 or x.numel() % head_dim or y.numel() != x.numel():
+        raise ValueError(f"RoPE: {tuple(x.shape)} is not a whole number of heads of {head_dim}")
+    half = cosine.shape[-1] if cosine.dim() else 0
+    if half:
+        tokens = cosine.numel() // half   # one row of the tables per token
+        if sine.numel() != cosine.numel() or tokens == 0 or x.numel() % (tokens * head_dim):
+            raise ValueError("RoPE: cosine/sine must hold [tokens, half] values for the tokens of x")
+        heads = x.numel() // (tokens * head_dim)
+    else:
+        tokens, heads = 1, x.numel() // head_dim
+    if x.numel() == 0:
+        return y
+    with torch.cuda.device(x.device):
+        status = _native.library().ct_rope(
+            _native.ptr(x), _native.ptr(y), _native.ptr(cosine), _native.ptr(sine), tokens, heads, head_dim, half,
+            int(inverse), int(rotated_only), _native.dtype_code(x.dtype), _native.dtype_code(cosine.dtype),
+            _native.stream_of(x))
+    _native.check(status, "ct_rope")
+    return y
+
+
+def rotate_owned_qk(query, key, cosine, sine, head_dim):
+    """Rotate newly allocated projection outputs before exposing them to autograd
+    (reference core_cuda.py:192-200): q [..., q_heads*head_dim] and k [..., k_heads*head_dim]
+    in place, positions from cosine/sine [tokens, half]."""
+    for tensor in (query, key):
+        _rope(tensor, tensor, cosine, sine, head_dim, inverse=False, rotated_only=True)
+
+
+def inverse_rope_tile(grad, cosine, sine, head_dim, output):
+    """Write an inverse rotation into a private tile, preserving caller gradients
+    (reference core_cuda.py:203-208)."""
+    return _rope(grad.contiguous(), output, cosine, sine, head_dim, inverse=True, rotated_only=False)
+
+
+class PartialRoPE(torch.autograd.Function):
+    """x [..., heads, head_dim] rotated on its first 2*half channels (reference
+    core_cuda.py:211-229)."""
+
+    @staticmethod
+    def forward(ctx, x, cosine, sine):
+        x = x.contiguous()
+        output = torch.empty_like(x)
+        ctx.head_dim = x.shape[-1]
+        ctx.save_for_backward(cosine, sine)
+        return _rope(x, output, cosine, sine, ctx.head_dim, inverse=False, rotated_only=False)
+
+    @staticmethod
+    def backward(ctx, grad):
+        cosine, sine = ctx.saved_tensors
+        grad = grad.contiguous()
+        output = torch.empty_like(grad)
+        return _rope(grad, output, cosine, sine, ctx.head_dim, inverse=True, rotated_only=False), None, None

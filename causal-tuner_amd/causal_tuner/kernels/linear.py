@@ -246,10 +246,10 @@ def can_fuse(module, x):
 class _Base:
     """The frozen base weight of one projection as the HIP GEMMs consume it.
 
-    A packed NF4 weight whose layout the fused loaders accept stays packed: every GEMM
-    decodes it tile by tile into LDS (bit-identical to `materialize`), so no dense copy is
-    written or re-read. Anything else is materialised once, as the reference does
-    (linear.py:70,107).
+    A packed NF4 weight whose layout the fused loaders accept is handed to the entry points
+    packed: below 512 rows every GEMM decodes it tile by tile into LDS, from 512 rows on the
+    entry point decodes it once into its workspace (both bit-identical to `materialize`).
+    Anything else is materialised here once, as the reference does (linear.py:70,107).
     """
 
     def __init__(self, weight, state, dtype):

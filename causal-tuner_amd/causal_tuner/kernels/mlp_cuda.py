@@ -4,7 +4,7 @@ Same operator API as the reference's kernels/mlp_cuda.py: `activation` (10-35, t
 `_activation` kernel, here `ct_silu_multiply`), `_SiLUMultiply` / `silu_multiply` (38-55),
 `_forward_into` (58-81), `_TiledLoRAMLP` (84-143) and `tiled_lora_mlp` (146-161). Gate, up and
 down are NF4-LoRA projections on the helpers of kernels/linear.py; a packed NF4 base stays
-packed (the GEMMs decode it in LDS) instead of being materialised per call.
+packed below 512 rows (the GEMMs decode it in LDS) and is decoded once per call above.
 """
 
 import torch

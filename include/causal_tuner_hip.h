@@ -24,6 +24,8 @@
  *   kernels/linear.py:84,125    torch.mm(x, a.T, out=xa)   -> ct_gemm (NT, bf16 out)
  *   kernels/linear.py:124,167   torch.mm(dy, b, out=low)   -> ct_gemm (NN, bf16 out)
  *   kernels/mlp_cuda.py:10-35   _activation (SiLU x up)    -> ct_silu_multiply
+ *   kernels/core_cuda.py:133-229 _rope / _owned_qk_rope     -> ct_rope
+ *                               (PartialRoPE, inverse_rope_tile, rotate_owned_qk)
  */
 #ifndef CAUSAL_TUNER_HIP_H
 #define CAUSAL_TUNER_HIP_H
@@ -199,6 +201,21 @@ int ct_accumulate(float *out, int64_t ldo,
  */
 int ct_silu_multiply(const void *gate, const void *up, void *h, void *dgate, void *dup, int64_t n,
                      int32_t backward, int32_t reconstruct, int32_t dtype, hipStream_t stream);
+
+/*
+ * Replaces the partial GPT-J rotary kernels `_rope` and `_owned_qk_rope` with
+ * `_rotate_pair` (kernels/core_cuda.py:133-189). x and y are [tokens, heads, head_dim]
+ * contiguous of `dtype` (CT_F32, CT_F16 or CT_BF16); cosine and sine are [tokens, half]
+ * contiguous of `trig_dtype`, half <= head_dim / 2. Channel pairs (2c, 2c+1), c < half:
+ *   e' = T(T(e cos) - T(o sin)),  o' = T(T(o cos) + T(e sin))    (T = round to dtype)
+ * with the sine negated when `inverse` (the backward rotation). With rotated_only = 0
+ * every pair is written to y (unrotated channels copied; y may be x); with rotated_only =
+ * 1 the rotation runs in place (y must be x) and other channels are not touched, as
+ * rotate_owned_qk does on freshly written projection outputs.
+ */
+int ct_rope(const void *x, void *y, const void *cosine, const void *sine, int64_t tokens, int64_t heads,
+            int64_t head_dim, int64_t half, int32_t inverse, int32_t rotated_only, int32_t dtype,
+            int32_t trig_dtype, hipStream_t stream);
 
 /*
  * Kernel timing for benchmarks; no counterpart in the reference (which publishes no kernel

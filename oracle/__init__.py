@@ -14,5 +14,7 @@ Contents (each function cites the reference file:line it restates):
                   xa and low and one final rounding of out and dx.
   mlp.py          the tiled LoRA MLP (SiLU-multiply with its bf16 rounding points, gate/up/
                   down projections, analytic backward) in float64.
+  rope.py         the partial GPT-J rotary embedding with its per-product rounding
+                  (numpy float32 + explicit round-to-nearest-even).
   nf4_dequant.c   plain-C decode, the timed CPU baseline (built by oracle/Makefile).
 """
