@@ -194,6 +194,71 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_any(
     }
 }
 
+// Transposed decode for the dx GEMM: out[c][r] = bf16(W[r][c]) for a [rows, cols] weight
+// (cols % 16 == 0, rows % 8 == 0, packed 8-byte aligned, blocksize >= 16). A workgroup
+// decodes a 64-row x 128-column tile: lane (p, c) reads 8 packed bytes (16 elements, one
+// block scale) of rows 2p and 2p+1, pairs the two rows' values into bf16x2 words and writes
+// them to LDS as [column][row pair]; the tile then leaves as 128 output rows of 128
+// contiguous bytes. The pair index is XORed with (column / 16 mod 4) * 8, which halves the
+// bank conflicts of the 4-byte LDS stores and keeps each 16-byte read contiguous.
+template <bool NESTED, int STORAGE>
+__global__ __launch_bounds__(kDequantThreads) void nf4_dequant_t(
+    const uint8_t *__restrict__ packed, const void *__restrict__ absmax_ptr, const float *__restrict__ code,
+    const float *__restrict__ code2, const float *__restrict__ absmax2, const float *__restrict__ offset_ptr,
+    uint16_t *__restrict__ out, int64_t rows, int64_t cols, int log2_block, int log2_block2) {
+    __shared__ float lds_code[16];
+    __shared__ float lds_code2[NESTED ? 256 : 1];
+    __shared__ uint32_t tile[128][32];
+    const int tid = threadIdx.x;
+    if (tid < 16) lds_code[tid] = code[tid];
+    if constexpr (NESTED) lds_code2[tid] = code2[tid];
+    __syncthreads();
+
+    const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 128;
+    const int unit = tid & 7, pair = tid >> 3;
+    const int64_t col = c0 + 16 * unit;
+    float v[2][16];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int64_t row = r0 + 2 * pair + h;
+        uint2 d = make_uint2(0, 0);
+        float s = 0.f;
+        if (row < rows && col < cols) {
+            const int64_t e = row * cols + col;
+            d = *reinterpret_cast<const uint2 *>(packed + (e >> 1));
+            const int64_t g = e >> log2_block;
+            if constexpr (NESTED) {
+                const uint8_t q = static_cast<const uint8_t *>(absmax_ptr)[g];
+                const float decoded = lds_code2[q] * absmax2[g >> log2_block2];
+                s = decoded + *offset_ptr;  // separately rounded add (no contraction)
+            } else {
+                s = static_cast<const float *>(absmax_ptr)[g];
+            }
+        }
+        const uint32_t words[2] = {d.x, d.y};
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const uint32_t byte = (words[b >> 2] >> (8 * (b & 3))) & 255u;
+            v[h][2 * b] = lds_code[byte >> 4] * s;
+            v[h][2 * b + 1] = lds_code[byte & 15u] * s;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int k = 16 * unit + i;
+        tile[k][pair ^ ((unit & 3) << 3)] = encode_pair<STORAGE, CT_BF16>(v[0][i], v[1][i]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = (tid >> 3) + 32 * j, chunk = tid & 7;
+        const int64_t oc = c0 + k, orow = r0 + 8 * chunk;
+        const u32x4 val = *reinterpret_cast<const u32x4 *>(&tile[k][(4 * chunk) ^ (((k >> 4) & 3) << 3)]);
+        if (oc < cols && orow < rows)
+            __builtin_nontemporal_store(val, reinterpret_cast<u32x4 *>(out + oc * rows + orow));
+    }
+}
+
 int log2_exact(int64_t v) {
     if (v <= 0 || (v & (v - 1))) return -1;
     int l = 0;
@@ -264,7 +329,47 @@ double dequant_bytes(const ct_nf4_weight *w, int64_t n, int out_dtype) {
     return bytes;
 }
 
+template <bool NESTED>
+hipError_t launch_transposed(const ct_nf4_weight *w, void *out, int lb, int lb2, hipStream_t stream) {
+    const dim3 grid((unsigned)cdiv(w->rows, 64), (unsigned)cdiv(w->cols, 128));
+    switch (w->storage_dtype) {
+        case CT_BF16:
+            nf4_dequant_t<NESTED, CT_BF16><<<grid, dim3(kDequantThreads), 0, stream>>>(
+                w->packed, w->absmax, w->code, w->code2, w->absmax2, w->offset, static_cast<uint16_t *>(out),
+                w->rows, w->cols, lb, lb2);
+            break;
+        case CT_F16:
+            nf4_dequant_t<NESTED, CT_F16><<<grid, dim3(kDequantThreads), 0, stream>>>(
+                w->packed, w->absmax, w->code, w->code2, w->absmax2, w->offset, static_cast<uint16_t *>(out),
+                w->rows, w->cols, lb, lb2);
+            break;
+        default:
+            nf4_dequant_t<NESTED, CT_F32><<<grid, dim3(kDequantThreads), 0, stream>>>(
+                w->packed, w->absmax, w->code, w->code2, w->absmax2, w->offset, static_cast<uint16_t *>(out),
+                w->rows, w->cols, lb, lb2);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
+
+// Whether nf4_dequant_transposed takes this weight (validated by validate_nf4 first).
+bool nf4_transposable(const ct_nf4_weight *w) {
+    return w->cols % 16 == 0 && w->rows % 8 == 0 && w->blocksize >= 16 &&
+           reinterpret_cast<uintptr_t>(w->packed) % 8 == 0 && cdiv(w->cols, 128) <= 65535;
+}
+
+// bf16 out[cols][rows] = the transpose of the decoded weight (same values as
+// ct_nf4_dequant with CT_BF16 output); out 16-byte aligned. Timed with the decoder family.
+hipError_t nf4_dequant_transposed(const ct_nf4_weight *w, void *out, hipStream_t stream) {
+    const int lb = log2_exact(w->blocksize);
+    const int lb2 = w->nested ? log2_exact(w->blocksize2) : 0;
+    const int slot = profile_open(CT_PROF_DEQUANT, stream);
+    const hipError_t e = w->nested ? launch_transposed<true>(w, out, lb, lb2, stream)
+                                   : launch_transposed<false>(w, out, lb, lb2, stream);
+    profile_close(slot, stream, dequant_bytes(w, w->rows * w->cols, CT_BF16));
+    return e;
+}
 
 // Host-side validation shared with the GEMM entry points.
 int validate_nf4(const ct_nf4_weight *w) {
