@@ -418,6 +418,47 @@ struct Fast<SRC_KS, ROWS, FRAG, THREADS> {
     }
 };
 
+// KT: 16-byte chunks of the operand's reduction rows, stored as loaded (k-major, swizzled
+// segments); consecutive lanes take consecutive chunks of one row, and a lane's chunks sit
+// in rows k, k + RS, k + 2 RS, ... (RS = rows per pass), which share one swizzle, so their
+// global and LDS addresses differ by constants.
+template <int ROWS, int FRAG, int THREADS>
+struct Fast<SRC_KT, ROWS, FRAG, THREADS> {
+    static constexpr int kRowChunks = ROWS / 8;
+    static constexpr int kPer = 64 * kRowChunks / THREADS;
+    static constexpr int kRowStep = THREADS / kRowChunks;  // rows covered by one pass of the lanes
+    static constexpr int kVmem = kPer, kWrites = kPer;
+    static_assert(kPer * THREADS == 64 * kRowChunks && THREADS % kRowChunks == 0 && kRowStep % 16 == 0 &&
+                      ROWS >= 128, "unsupported KT tile");
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t off0, pitch;
+    int k_first, byte0, kext;
+    bool ok;
+    uint4 v[kPer];
+    __device__ __forceinline__ void init(const Operand &o, int64_t rows, int64_t kext_, int64_t r0, int tid) {
+        const uint16_t *p = static_cast<const uint16_t *>(o.p) + r0;
+        r = make_rsrc(p, kext_ > 0 ? ((kext_ - 1) * o.ld + (rows - r0)) * 2 : 0);
+        kext = (int)kext_;
+        pitch = (uint32_t)(o.ld * 2);
+        const int cc = tid % kRowChunks;
+        k_first = tid / kRowChunks;
+        ok = r0 + 8 * cc < rows;
+        off0 = (uint32_t)(k_first * o.ld + 8 * cc) * 2;
+        byte0 = kt_byte<ROWS>(k_first, 8 * cc);
+    }
+    __device__ __forceinline__ void issue(uint4 *, int64_t k0) {
+        const uint32_t base = off0 + (uint32_t)k0 * pitch;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+            v[i] = buf_load16(r, (ok && (int)k0 + k_first + i * kRowStep < kext) ? base + i * kRowStep * pitch : kOOB);
+    }
+    __device__ __forceinline__ void commit(uint4 *stage, const float *, const float *, float) const {
+        char *b = reinterpret_cast<char *>(stage) + byte0;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) *reinterpret_cast<uint4 *>(b + i * kRowStep * (ROWS * 2)) = v[i];
+    }
+};
+
 // NF4 (nested), reduction along the weight's columns: units of 32 elements of one row.
 template <int ROWS, int FRAG, int THREADS>
 struct Fast<SRC_NF4, ROWS, FRAG, THREADS> {
@@ -602,7 +643,10 @@ struct FastRunner {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-            for (int i = 0; i < FM; ++i) af[ks][i] = cur[slot(wm0 + i * 16 + (lane & 15), ks * 4 + (lane >> 4))];
+            for (int i = 0; i < FM; ++i) {
+                if constexpr (SA == SRC_KT) af[ks][i] = kt_fragment<BM>(cur, wm0 + i * 16, ks * 32, lane);
+                else af[ks][i] = cur[slot(wm0 + i * 16 + (lane & 15), ks * 4 + (lane >> 4))];
+            }
         la.commit(nxt, lcode, lcode2, off_a);
         lb.commit(nxt + BM * 8, lcode, lcode2, off_b);
         la.issue(nxt, knext);
@@ -611,8 +655,10 @@ struct FastRunner {
         for (int j = 0; j < FN; ++j) {
             uint4 bf[KS];
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                bf[ks] = cur[BM * 8 + slot(wn0 + j * 16 + (lane & 15), ks * 4 + (lane >> 4))];
+            for (int ks = 0; ks < KS; ++ks) {
+                if constexpr (SB == SRC_KT) bf[ks] = kt_fragment<BN>(cur + BM * 8, wn0 + j * 16, ks * 32, lane);
+                else bf[ks] = cur[BM * 8 + slot(wn0 + j * 16 + (lane & 15), ks * 4 + (lane >> 4))];
+            }
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
@@ -687,9 +733,15 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     const int64_t m0 = (int64_t)tm * BM;
     // Grouped products: the tile's operands, its column offset inside them and its column
     // count; `out_shift` moves its output columns past group 0.
-    constexpr bool kGrouped = OUT == CT_F32 && A0 == SRC_KS && B0 == SRC_KS;  // the parameter gradients
+    constexpr bool kGrouped = OUT == CT_F32 && (A0 == SRC_KS || A0 == SRC_KT) &&
+                              (B0 == SRC_KS || B0 == SRC_KT);  // the parameter gradients
     const bool second = kGrouped && p.group_tiles > 0 && tn >= p.group_tiles;
-    const Segment &sg0 = second ? p.seg[1] : p.seg[0];
+    // Copied by a branch on the (uniform) condition: a reference chosen by a select would
+    // move the kernel argument to private memory and make every descriptor built from it
+    // look divergent (a readfirstlane loop around each buffer load).
+    Segment sg0;
+    if (second) sg0 = p.seg[1];
+    else sg0 = p.seg[0];
     const int64_t n0 = (int64_t)(second ? tn - p.group_tiles : tn) * BN;
     const int64_t ncols = second ? p.n1 : p.n;
     const int64_t out_shift = second ? (int64_t)p.group_tiles * BN : 0;
@@ -730,6 +782,33 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     }
 
     // ------------------------------------------------------------------ epilogue
+    if constexpr (B0 == SRC_KT) {
+        // KT B fragments leave lane l with columns wn0 + 16 j + (l % 16): element stores.
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int64_t row = m0 + wm0 + i * 16 + (lane >> 4) * 4 + e;
+                if (row >= p.m) continue;
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const int64_t col = n0 + wn0 + 16 * j + (lane & 15);
+                    if (col >= ncols) continue;
+                    const float bias = p.bias ? bf16_to_f32(p.bias[col]) : 0.f;
+                    const float v = acc[i][j][e] + bias;
+                    if constexpr (OUT == CT_F32) {
+                        float *c = static_cast<float *>(p.c) + (int64_t)blockIdx.z * p.split_stride + row * p.ldc +
+                                   out_shift + col;
+                        *c = p.beta ? v + *c : v;
+                    } else {
+                        uint16_t *c = static_cast<uint16_t *>(p.c) + row * p.ldc + out_shift + col;
+                        *c = bf16_bits(p.beta ? v + bf16_to_f32(*c) : v);
+                    }
+                }
+            }
+        }
+        return;
+    }
     // Lane l holds rows wm0 + 16 i + 4 (l / 16) + e and columns wn0 + FN (l % 16) + j.
     const int64_t col = n0 + wn0 + (lane & 15) * FN;
     float bias[FN];
@@ -888,7 +967,7 @@ struct Problem {
 
 // Byte extent of a dense operand whose output-dimension extent is `rows`.
 int64_t dense_extent(const Operand &o, int src, int64_t rows, int64_t k) {
-    return src == SRC_KS ? ((k > 0 ? k - 1 : 0) * o.ld + rows) * 2 : rows * o.ld * 2;
+    return (src == SRC_KS || src == SRC_KT) ? ((k > 0 ? k - 1 : 0) * o.ld + rows) * 2 : rows * o.ld * 2;
 }
 
 bool aligned16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
@@ -909,8 +988,8 @@ bool vec_ok(const Problem &pr) {
         if (g.k % 8) return false;
         if (!is_nf4_host(sa) && (!aligned16(g.a.p) || g.a.ld % 8)) return false;
         if (!is_nf4_host(sb) && (!aligned16(g.b.p) || g.b.ld % 8)) return false;
-        if (sa == SRC_KS && p.m % 8) return false;
-        if (sb == SRC_KS && segment_cols(p, s) % 8) return false;
+        if ((sa == SRC_KS || sa == SRC_KT) && p.m % 8) return false;
+        if ((sb == SRC_KS || sb == SRC_KT) && segment_cols(p, s) % 8) return false;
     }
     if (!aligned16(p.c) || p.ldc % 8) return false;
     return true;
@@ -958,6 +1037,19 @@ hipError_t launch_cfg(const GemmParams &p0, int tile, int splits, hipStream_t s)
     else if (tile == TILE_256) gemm_big<A0, B0, A1, B1, MODE, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
     else if (tile == TILE_128) gemm_small<128, 128, A0, B0, A1, B1, MODE, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
     else gemm_small<64, 64, A0, B0, A1, B1, MODE, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
+    return hipGetLastError();
+}
+
+// One fixed tile on the fast runner (operand sources the generic runner does not have).
+template <int A0, int B0, int A1, int B1, int OUT, int TILE>
+hipError_t launch_cfg_fast(const GemmParams &p0, int splits, hipStream_t s) {
+    GemmParams p = p0;
+    constexpr int e = TILE == TILE_256 ? 256 : 128;
+    p.tiles_m = (int)cdiv(p.m, e);
+    p.tiles_n = (int)(p.group_tiles > 0 ? p.group_tiles + cdiv(p.n1, e) : cdiv(p.n, e));
+    dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)splits);
+    if constexpr (TILE == TILE_256) gemm_big8<A0, B0, A1, B1, OUT><<<grid, dim3(512), 0, s>>>(p);
+    else gemm_small<128, 128, A0, B0, A1, B1, 2, OUT><<<grid, dim3(kThreads), 0, s>>>(p);
     return hipGetLastError();
 }
 
@@ -1010,6 +1102,12 @@ hipError_t run(Problem &pr, hipStream_t s) {
             return launch_vec_out<SRC_KS, SRC_KS, SRC_KS, SRC_KS>(pr, tile, s);
         case CT_LAYOUT(SRC_KS, SRC_KC, SRC_KS, SRC_KC):
             return launch_vec_out<SRC_KS, SRC_KC, SRC_KS, SRC_KC>(pr, tile, s);
+        case CT_LAYOUT(SRC_KT, SRC_KT, SRC_KT, SRC_KT):
+            // Fast runner only, fp32 output, tiles of at least 128 (the parameter gradients).
+            if (!fast_ok(pr) || pr.out != CT_F32 || tile == TILE_64) return hipErrorInvalidValue;
+            if (tile == TILE_256)
+                return launch_cfg_fast<SRC_KT, SRC_KT, SRC_KT, SRC_KT, CT_F32, TILE_256>(pr.p, pr.splits, s);
+            return launch_cfg_fast<SRC_KT, SRC_KT, SRC_KT, SRC_KT, CT_F32, TILE_128>(pr.p, pr.splits, s);
         // NF4 loaders keep their own alignment (checked by nf4_fusable); VEC covers the
         // dense operands and the output.
         case CT_LAYOUT(SRC_KC, SRC_NF4, SRC_KC, SRC_KC):
@@ -1545,11 +1643,17 @@ extern "C" int ct_parameter_gradients(const void *x, int64_t ldx, const void *dy
     pr.p.c = workspace;
     pr.p.ldc = pl.width;
     pr.p.split_stride = r * pl.width;
-    pr.src[0] = pr.src[1] = pr.src[2] = pr.src[3] = SRC_KS;
+    // Both operands are token-major. On the fast path they enter LDS as loaded (KT) and the
+    // MFMA fragments come from transpose reads; otherwise the registers transpose them (KS).
+    pr.src[0] = pr.src[1] = pr.src[2] = pr.src[3] = SRC_KT;
     pr.out = CT_F32;
     pr.splits = pl.splits;
     pr.tile = pl.tile;
     pr.vec = vec_ok(pr);
+    if (pl.tile == TILE_64 || !fast_ok(pr)) {
+        pr.src[0] = pr.src[1] = pr.src[2] = pr.src[3] = SRC_KS;
+        pr.vec = vec_ok(pr);
+    }
     hipError_t e = run(pr, stream);
     if (e == hipSuccess) {
         const int64_t gcols = k > 0 ? (int64_t)pl.gt * kTileEdge[pl.tile] : 0;

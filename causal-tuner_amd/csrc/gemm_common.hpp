@@ -6,7 +6,10 @@
 
 namespace ct {
 
-enum Src { SRC_KC = 0, SRC_KS = 1, SRC_NF4 = 2, SRC_NF4T = 3 };
+// Operand sources: KC reduction-contiguous bf16; KS output-contiguous bf16 transposed in
+// registers on its way to LDS; NF4/NF4T packed weights; KT output-contiguous bf16 stored
+// in LDS as loaded (one LDS row per reduction index) and transposed by the fragment reads.
+enum Src { SRC_KC = 0, SRC_KS = 1, SRC_NF4 = 2, SRC_NF4T = 3, SRC_KT = 4 };
 
 struct Operand {
     const void *p;        // bf16 elements, or packed NF4 bytes
@@ -87,6 +90,37 @@ __device__ __forceinline__ int frag_row_inv(int s) {
     if constexpr (FRAG == 1) return s;
     constexpr int W = 16 * FRAG;
     return (s & ~(W - 1)) | ((s & 15) * FRAG) | ((s % W) >> 4);
+}
+
+// KT tiles: LDS row k holds the COLS output-side elements of reduction index k (COLS * 2
+// bytes), its 32-byte segments XORed with kt_swizzle(k). A fragment read (two
+// ds_read_b64_tr_b16) has its lanes address rows k0 + 8 (l / 16) + (l % 16) / 4 at
+// 32-byte segment columns; under this swizzle those reads are conflict-free (measured on
+// MI355X: 117 B/clk per CU, the rate of linear 8-byte reads).
+__device__ __forceinline__ int kt_swizzle(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
+template <int COLS>
+__device__ __forceinline__ int kt_byte(int k, int e) {
+    static_assert(COLS >= 128, "KT tiles need at least 8 segments per row");
+    return k * (COLS * 2) + (((e >> 4) ^ kt_swizzle(k)) << 5) + ((e & 15) << 1);
+}
+typedef short kt_v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) kt_v4s lds_kt_v4s;
+// The MFMA operand of 16 output-side elements c0 .. c0+15 and reduction indices
+// k0 + 8 (l / 16) + 0..7 from a KT tile: lane i of each 16-lane group receives element
+// c0 + i at 4 consecutive k per transpose read.
+// k0 must be a multiple of 32: the swizzle of rows k0 + lk (+ 4) then depends on the lane
+// alone, so the k0 and second-read parts of the address are immediate offsets.
+template <int COLS>
+__device__ __forceinline__ uint4 kt_fragment(const uint4 *tile, int c0, int k0, int lane) {
+    const int g = lane >> 4, j = lane & 15;
+    const int lk = 8 * g + (j >> 2);
+    const int base = lk * (COLS * 2) + (((c0 >> 4) ^ kt_swizzle(lk)) << 5) + ((j & 3) << 3);
+    const __attribute__((address_space(3))) char *b =
+        (const __attribute__((address_space(3))) char *)tile + k0 * (COLS * 2) + base;
+    const kt_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_kt_v4s *)b);
+    const kt_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_kt_v4s *)(b + 4 * (COLS * 2)));
+    const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+    return make_uint4(l2.x, l2.y, h2.x, h2.y);
 }
 
 // Eight nibbles of one packed dword -> eight bf16 (element 2j from the high nibble of byte j).
