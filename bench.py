@@ -15,9 +15,11 @@ roofline  the dominant kernel family, timed with HIP events around each of its l
           traffic from profiles/<family>_traffic.json (rocprofv3 --pmc, see --pmc-summary).
 kernels   the same per-family breakdown for every timed family.
 dequant   C2: standalone NF4 dequant, GB/s against the 8 TB/s HBM peak.
+projections  C1 and C5: one projection fwd+bwd at several row counts, with the bound that
+          applies (HBM for few rows, bf16 MFMA for many).
 cpu_baseline  the reference's op sequence on the host CPU (oracle/lora.py), bounded sample.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-dequant]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-dequant] [--no-sweep]
     python bench.py --copy-probe MiB ...     # first run a plain copy of that size (PMC scale)
     python bench.py --pmc-summary FETCH.csv WRITE.csv FAMILY MiB   # write profiles/FAMILY_traffic.json
 """
@@ -140,6 +142,50 @@ def dequant_measure(device):
     return results
 
 
+def skinny_bytes(m, k, n, r):
+    """Algorithmic HBM bytes of one projection fwd+bwd (NF4 base): the packed weight read in
+    both passes, A and B fp32 read twice, dA and dB fp32 written once, x read twice, y, dy
+    and dx once."""
+    s_nf4 = k * n * (0.5 + 1 / 64 + 1 / 4096)
+    return 2 * s_nf4 + 12 * r * (k + n) + 2 * m * (3 * k + 2 * n)
+
+
+def projection_measure(device, shapes, rows_list, iters=20, rank=R):
+    """One NF4-LoRA projection fwd+bwd through project_group + autograd (the reference's
+    operator path), per shape and row count: average ms over `iters` steps (HIP events),
+    algorithmic TFLOP/s and GB/s, and the fraction of the bound that applies (HBM for
+    few rows, bf16 MFMA for many)."""
+    from causal_tuner.kernels.linear import project_group
+    from causal_tuner.modeling.lora import Projection
+    results = {}
+    for k, n in shapes:
+        torch.manual_seed(2)
+        module = Projection(k, n, rank=rank, device=device)
+        module.install_nf4(module.weight.detach().clone(), device)
+        torch.nn.init.normal_(module.lora_B, std=0.01)
+        g = torch.Generator(device=device).manual_seed(3)
+        for m in rows_list:
+            x = torch.randn(m, k, device=device, generator=g).to(torch.bfloat16).requires_grad_(True)
+            dy = torch.randn(m, n, device=device, generator=g).to(torch.bfloat16)
+
+            def step():
+                out, = project_group((module,), x)
+                torch.autograd.grad(out, (x, module.lora_A, module.lora_B), dy)
+            ms = time_events(step, iters)
+            flops, nbytes = projection_flops(m, k, n, rank), skinny_bytes(m, k, n, rank)
+            tflops, gbs = flops / (ms * 1e-3) / 1e12, nbytes / (ms * 1e-3) / 1e9
+            bound = "hbm" if flops / nbytes < BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma"
+            frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tflops / BF16_PEAK_TFLOPS
+            results[f"{k}->{n} M{m}"] = {"ms": round(ms, 4), "TFLOP/s": round(tflops, 2), "GB/s": round(gbs, 1),
+                                         "bound": bound, "frac": round(frac, 4)}
+            log(f"  {k}->{n} M={m:6d}: {ms:8.3f} ms  {tflops:8.2f} TFLOP/s  {gbs:8.1f} GB/s  "
+                f"{bound} {100 * frac:.1f}%")
+            del x, dy
+        del module
+        torch.cuda.empty_cache()
+    return results
+
+
 def cpu_baseline(budget_s=12.0):
     """The reference's torch-op sequence (oracle/lora.py) on the host CPU, bf16, for the
     seven C3 projections over a bounded token sample."""
@@ -186,8 +232,10 @@ FAMILIES = {
     "dequant": ("CT_PROF_DEQUANT", "in-step NF4 decode of the base weights (ct_nf4_dequant, bytes not flops)"),
 }
 # The dx family is one kernel instantiation for every C3 projection (all reach 256x256 tiles).
-KERNEL_NAMES = {"dx_gemm": "gemm_big8<KC, KS, KC, KS>", "fwd_gemm": "gemm_big8<KC, KC, KC, KC> (q,o,gate,up,down) "
-                "+ gemm_small<64,64,...> (k, v)"}
+# At 8192 rows the dx GEMM runs on the transposed decoded weight, so both big GEMM families
+# share one kernel instantiation.
+KERNEL_NAMES = {"dx_gemm": "gemm_big8<KC, KC, KC, KC> (dx on w^T and a^T)",
+                "fwd_gemm": "gemm_big8<KC, KC, KC, KC> (q,o,gate,up,down) + gemm_small<64,64,...> (k, v)"}
 
 
 def traffic_from_profiles(kernel_key):
@@ -214,7 +262,8 @@ def pmc_summary(fetch_csv, write_csv, family, mib):
     """Per-launch HBM traffic of a kernel family from two rocprofv3 --pmc runs (FETCH_SIZE,
     WRITE_SIZE, KiB per dispatch), each scaled by the same counter's reading for the copy
     probe of `mib` MiB; written to profiles/<family>_traffic.json."""
-    patterns = {"dx_gemm": "gemm_big8<0, 1, 0, 1, 2>", "fwd_gemm": "gemm_big8<0, 0, 0, 0, 2>"}
+    # Forward and dx share the instantiation: the figure averages both families' launches.
+    patterns = {"dx_gemm": "gemm_big8<0, 0, 0, 0, 2>", "fwd_gemm": "gemm_big8<0, 0, 0, 0, 2>"}
     copy_bytes = mib << 20
 
     def read(path, counter):
@@ -255,6 +304,7 @@ def main():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--no-dequant", action="store_true", help="skip the standalone dequant leg")
+    parser.add_argument("--no-sweep", action="store_true", help="skip the C1/C5 projection legs")
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MiB",
                         help="first run a plain device copy of this size (scales PMC byte counters)")
     args = parser.parse_args()
@@ -316,6 +366,11 @@ def main():
 
     dequant = None if args.no_dequant else dequant_measure(device)
     log(f"dequant: {dequant}")
+    sweep = None
+    if not args.no_sweep:
+        log("C1 and C5 projections (fwd+bwd, NF4 base, one projection):")
+        sweep = {"C1": projection_measure(device, [(1024, 1024)], [512], rank=16),
+                 "C5": projection_measure(device, [(6144, 24576), (24576, 6144)], [16, 64, 256, 16384], iters=10)}
     cpu = None if args.no_cpu else cpu_baseline()
     log(f"cpu baseline: {cpu}")
 
@@ -334,6 +389,9 @@ def main():
         "kernels": families,
         "dequant": {"workload": "C2: standalone NF4 dequant to bf16", "bound": "hbm", "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "results": dequant},
+        "projections": {"workload": "C1 (M 512, 1024->1024, rank 16) and C5 (6144<->24576, M 16..16384, rank "
+                                    "256): one NF4-LoRA projection fwd+bwd through project_group + autograd",
+                        "results": sweep},
     }
     print(json.dumps(line), flush=True)
 

@@ -797,8 +797,9 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
                     const float bias = p.bias ? bf16_to_f32(p.bias[col]) : 0.f;
                     const float v = acc[i][j][e] + bias;
                     if constexpr (OUT == CT_F32) {
-                        float *c = static_cast<float *>(p.c) + (int64_t)blockIdx.z * p.split_stride + row * p.ldc +
-                                   out_shift + col;
+                        float *c = (second && p.c1) ? p.c1 + col * p.ldc1 + row
+                                                    : static_cast<float *>(p.c) + (int64_t)blockIdx.z * p.split_stride +
+                                                          row * p.ldc + out_shift + col;
                         *c = p.beta ? v + *c : v;
                     } else {
                         uint16_t *c = static_cast<uint16_t *>(p.c) + row * p.ldc + out_shift + col;
@@ -1643,6 +1644,8 @@ extern "C" int ct_parameter_gradients(const void *x, int64_t ldx, const void *dy
     pr.p.c = workspace;
     pr.p.ldc = pl.width;
     pr.p.split_stride = r * pl.width;
+    // One split on the KT path: the kernel writes dA and dB (transposed) itself.
+    const bool direct = pl.splits == 1 && k > 0 && n > 0;
     // Both operands are token-major. On the fast path they enter LDS as loaded (KT) and the
     // MFMA fragments come from transpose reads; otherwise the registers transpose them (KS).
     pr.src[0] = pr.src[1] = pr.src[2] = pr.src[3] = SRC_KT;
@@ -1653,6 +1656,16 @@ extern "C" int ct_parameter_gradients(const void *x, int64_t ldx, const void *dy
     if (pl.tile == TILE_64 || !fast_ok(pr)) {
         pr.src[0] = pr.src[1] = pr.src[2] = pr.src[3] = SRC_KS;
         pr.vec = vec_ok(pr);
+    }
+    if (direct && pr.src[0] == SRC_KT) {
+        pr.p.c = da;
+        pr.p.ldc = k;
+        pr.p.beta = add;
+        pr.p.c1 = db;
+        pr.p.ldc1 = r;
+        const hipError_t e = run(pr, stream);
+        profile_close(slot, stream, 2.0 * m * r * (double)(k + n));
+        return to_status(e);
     }
     hipError_t e = run(pr, stream);
     if (e == hipSuccess) {

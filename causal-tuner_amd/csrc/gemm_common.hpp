@@ -45,6 +45,10 @@ struct GemmParams {
     // group_tiles * BN on.
     int group_tiles;
     int64_t n1;
+    // Grouped mode with one split: group 1 is written transposed to c1 (element (i, c) at
+    // c1[c * ldc1 + i]) instead of next to group 0.
+    float *c1;
+    int64_t ldc1;
 };
 
 // ------------------------------------------------------------------ LDS layout and NF4 decode

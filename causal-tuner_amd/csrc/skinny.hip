@@ -21,6 +21,8 @@
 // transposed through a wave-private LDS tile [16*NB columns][128 + 8] (the padding
 // spreads columns over banks); no workgroup barrier is needed for them.
 
+#include <cstdlib>
+
 #include "gemm_common.hpp"
 
 namespace ct {
@@ -300,7 +302,14 @@ struct SkStage<SRC_NF4T, MB, NB> {
     }
 };
 
-// One segment: this wave's contiguous range of k-blocks, loads one block ahead.
+// k-blocks in flight while one is computed: two for the row-streaming sources with few
+// rows (their register stages are small and HBM latency dominates), one otherwise.
+template <int SB, int MB, int NB>
+constexpr int sk_depth() {
+    return (!transposed_src(SB) && MB * NB <= 2) ? 2 : 1;
+}
+
+// One segment: this wave's contiguous range of k-blocks, loads one or two blocks ahead.
 template <int SB, int MB, int NB>
 __device__ __forceinline__ void sk_segment(const Segment &sg, int64_t m, int64_t n, int64_t n0, int wave, int lane,
                                            f32x4 (&acc)[MB][NB], char *tile, const float *lcode,
@@ -317,26 +326,51 @@ __device__ __forceinline__ void sk_segment(const Segment &sg, int64_t m, int64_t
     const float offset = is_nf4_src(SB) ? *sg.b.offset : 0.f;
     SkStage<SB, MB, NB> st;
     st.init(sg.b, n, n0, sg.k);
-    SkA<MB> a;
-    a.load(ra, sg.a.ld, (int)sg.k, kb0, g, c);
-    st.load(kb0, g, c, lane);
-    for (int kb = kb0; kb < kb1; ++kb) {
-        SkA<MB> an = a;
-        SkStage<SB, MB, NB> sn = st;
-        if (kb + 1 < kb1) {  // wave-uniform
-            an.load(ra, sg.a.ld, (int)sg.k, kb + 1, g, c);
-            sn.load(kb + 1, g, c, lane);
-        }
+    const auto compute = [&](const SkA<MB> &a, const SkStage<SB, MB, NB> &stage) {
         uint4 b[NB][4];
-        st.frags(b, tile, lcode, lcode2, offset, g, c);
+        stage.frags(b, tile, lcode, lcode2, offset, g, c);
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
             for (int mi = 0; mi < MB; ++mi)
 #pragma unroll
                 for (int nj = 0; nj < NB; ++nj) acc[mi][nj] = mfma16x16x32(a.f[mi][s], b[nj][s], acc[mi][nj]);
-        a = an;
-        st = sn;
+    };
+    const auto fetch = [&](SkA<MB> &a, SkStage<SB, MB, NB> &stage, int kb) {
+        if (kb < kb1) {  // wave-uniform
+            a.load(ra, sg.a.ld, (int)sg.k, kb, g, c);
+            stage.load(kb, g, c, lane);
+        }
+    };
+    if constexpr (sk_depth<SB, MB, NB>() == 2) {
+        // Two k-blocks in flight: three register stages in rotation, the loop unrolled by
+        // three so every stage keeps its registers.
+        SkA<MB> a0, a1, a2;
+        SkStage<SB, MB, NB> s0 = st, s1 = st, s2 = st;
+        fetch(a0, s0, kb0);
+        fetch(a1, s1, kb0 + 1);
+        for (int kb = kb0; kb < kb1; kb += 3) {
+            fetch(a2, s2, kb + 2);
+            compute(a0, s0);
+            if (kb + 1 >= kb1) break;
+            fetch(a0, s0, kb + 3);
+            compute(a1, s1);
+            if (kb + 2 >= kb1) break;
+            fetch(a1, s1, kb + 4);
+            compute(a2, s2);
+        }
+    } else {
+        SkA<MB> a;
+        a.load(ra, sg.a.ld, (int)sg.k, kb0, g, c);
+        st.load(kb0, g, c, lane);
+        for (int kb = kb0; kb < kb1; ++kb) {
+            SkA<MB> an = a;
+            SkStage<SB, MB, NB> sn = st;
+            fetch(an, sn, kb + 1);
+            compute(a, st);
+            a = an;
+            st = sn;
+        }
     }
 }
 
@@ -424,6 +458,9 @@ SkShape sk_shape(const GemmParams &p, bool transposed, int64_t ws_floats) {
     int nb;
     if (transposed) nb = mb <= 2 ? 4 : 2;
     else nb = (mb <= 2 && cdiv(p.n, 64) >= 128) ? 4 : (cdiv(p.n, 32) >= 128 ? 2 : 1);
+#ifdef CT_TUNING
+    if (const char *env = getenv(transposed ? "CT_SKNB_T" : "CT_SKNB")) nb = atoi(env);
+#endif
     const int64_t wgs = cdiv(p.n, 16 * nb);
     int64_t nkb = 0;
     for (int s = 0; s < p.nseg; ++s) nkb = nkb > cdiv(p.seg[s].k, kKB) ? nkb : cdiv(p.seg[s].k, kKB);
