@@ -108,6 +108,14 @@ def dtype_code(dtype):
         raise ValueError(f"Unsupported element type {dtype}") from None
 
 
+def nf4_kind(desc):
+    """The `nf4` argument of the workspace queries: 0 for a bf16 weight, 1 for a
+    double-quantized NF4 weight, 2 for NF4 with plain absmax."""
+    if desc is None:
+        return 0
+    return 1 if desc.nested else 2
+
+
 def nf4_descriptor(weight, state):
     """Build the ct_nf4_weight view of a packed weight and its QuantState (no copies)."""
     nested = bool(state.nested)

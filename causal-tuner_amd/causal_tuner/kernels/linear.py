@@ -156,7 +156,7 @@ def _forward(x, weight, state, a, b, bias, out, xa):
     target, low = _Output(out), _Contiguous(xa)
     desc = None if state is None else _native.nf4_descriptor(w, state)
     lib = _native.library()
-    ws = _workspace(lib.ct_forward_linear_workspace(m, n, k, r, int(desc is not None)), x.device)
+    ws = _workspace(lib.ct_forward_linear_workspace(m, n, k, r, _native.nf4_kind(desc)), x.device)
     with torch.cuda.device(x.device):
         status = lib.ct_forward_linear(
             _native.ptr(x), ldx, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),
@@ -192,7 +192,7 @@ def _input_gradient(dy, weight, state, a, b, dx, low, add):
         target.buffer.copy_(dx)
     desc = None if state is None else _native.nf4_descriptor(w, state)
     lib = _native.library()
-    ws = _workspace(lib.ct_input_gradient_workspace(m, n, k, r, int(desc is not None)), dy.device)
+    ws = _workspace(lib.ct_input_gradient_workspace(m, n, k, r, _native.nf4_kind(desc)), dy.device)
     with torch.cuda.device(dy.device):
         status = lib.ct_input_gradient(
             _native.ptr(dy), lddy, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),

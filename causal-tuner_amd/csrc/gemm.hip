@@ -888,16 +888,26 @@ __global__ __launch_bounds__(512) void gemm_big8(const GemmParams p) {
     gemm_body<256, 256, A0, B0, A1, B1, 2, OUT, 4, 2>(p);
 }
 
-// Deterministic reduction of fp32 split partials: out = sum_z ws[z] (+ out), in z order.
+// Deterministic reduction of fp32 split partials: out = sum_z ws[z] (+ bias) (+ out), in
+// z order. Grid: (column blocks of 256, rows); eight partials in flight per thread (they
+// were written by other XCDs and come from memory).
 template <int OUT>
 __global__ __launch_bounds__(256) void reduce_splits(const float *__restrict__ ws, int splits, int64_t stride,
-                                                     int64_t rows, int64_t cols, void *out, int64_t ldo,
-                                                     int add) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= rows * cols) return;
-    const int64_t r = i / cols, c = i % cols;
-    float s = ws[i];
-    for (int z = 1; z < splits; ++z) s += ws[z * stride + i];
+                                                     int64_t rows, int64_t cols, void *out, int64_t ldo, int add,
+                                                     const uint16_t *__restrict__ bias) {
+    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
+    if (c >= cols) return;
+    const int64_t i = r * cols + c;
+    float s = 0.f;
+    for (int z0 = 0; z0 < splits; z0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = z0 + j < splits ? ws[(z0 + j) * stride + i] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (z0 + j < splits) s = (z0 + j == 0) ? v[j] : s + v[j];
+    }
+    if (bias) s += bf16_to_f32(bias[c]);
     if constexpr (OUT == CT_F32) {
         float *o = static_cast<float *>(out) + r * ldo + c;
         *o = add ? s + *o : s;
@@ -954,6 +964,30 @@ __global__ __launch_bounds__(256) void reduce_param(const float *__restrict__ ws
 // ------------------------------------------------------------------------ host side
 enum Tile { TILE_256 = 0, TILE_128 = 1, TILE_64 = 2 };
 constexpr int kTileEdge[3] = {256, 128, 64};
+
+#ifndef CT_MATERIALIZE_ROWS
+#define CT_MATERIALIZE_ROWS 512
+#endif
+// An NF4 base weight is decoded inside the GEMM's operand loader only while the rows are
+// few: each 256-row tile decodes its slice of the weight again, and from kMaterializeRows
+// rows on one ct_nf4_dequant pass into the workspace (the reference's materialize) plus
+// the dense GEMM is faster. Both give identical results.
+constexpr int64_t kMaterializeRows = CT_MATERIALIZE_ROWS;
+// Rows between the few-row kernels (m <= 64) and kMaterializeRows: the output alone
+// leaves most CUs idle, so the 256 x 256 fast runner splits the reduction and the fp32
+// partials are added in split order (with bias and beta) by reduce_splits. The split
+// count depends only on the shapes.
+int mid_splits(int64_t m, int64_t n, int64_t ktot) {
+    if (m <= 64 || m >= kMaterializeRows || n <= 0) return 1;
+    // One round of the one-per-CU 256 x 256 workgroups: a partial second round would
+    // take as long as the first.
+    const int64_t tiles = cdiv(m, 256) * cdiv(n, 256);
+    int64_t s = 256 / tiles;
+    const int64_t cap = cdiv(ktot, kBK) / 8;  // at least 8 k-tiles per split
+    if (s > cap) s = cap;
+    if (s > 16) s = 16;
+    return (int)(s < 1 ? 1 : s);
+}
 
 struct Problem {
     GemmParams p;
@@ -1081,6 +1115,28 @@ hipError_t run(Problem &pr, hipStream_t s) {
         pr.src[2] = pr.src[0];
         pr.src[3] = pr.src[1];
     }
+    if (pr.splits == 1 && pr.out == CT_BF16 && p.group_tiles == 0 && p.m > 64) {
+        const int splits = mid_splits(p.m, p.n, p.seg[0].k + (p.nseg > 1 ? p.seg[1].k : 0));
+        const int64_t need = (int64_t)splits * p.m * p.n * 4;
+        if (splits > 1 && fast_ok(pr) && pr.ws && pr.ws_bytes >= need && aligned16(pr.ws) && p.n % 8 == 0) {
+            Problem q = pr;
+            q.splits = splits;
+            q.out = CT_F32;
+            q.tile = TILE_256;
+            q.ws = nullptr;
+            q.ws_bytes = 0;
+            q.p.c = pr.ws;
+            q.p.ldc = p.n;
+            q.p.split_stride = p.m * p.n;
+            q.p.beta = 0;
+            q.p.bias = nullptr;
+            const hipError_t e = run(q, s);
+            if (e != hipSuccess) return e;
+            reduce_splits<CT_BF16><<<dim3((unsigned)cdiv(p.n, 256), (unsigned)p.m), 256, 0, s>>>(
+                static_cast<const float *>(pr.ws), splits, p.m * p.n, p.m, p.n, p.c, p.ldc, p.beta, p.bias);
+            return hipGetLastError();
+        }
+    }
     if (pr.splits == 1 && pr.out == CT_BF16 && p.m <= 64) {
         // Few rows: the workgroup streams the weight with its 8 waves splitting the reduction.
         const int sa[2] = {pr.src[0], pr.src[2]}, sb[2] = {pr.src[1], pr.src[3]};
@@ -1093,7 +1149,9 @@ hipError_t run(Problem &pr, hipStream_t s) {
     const int64_t tiles = total_tiles(p);
     p.tiles_per_split = cdiv(tiles > 0 ? tiles : 1, pr.splits);
     const bool nf4 = is_nf4_host(pr.src[0]) || is_nf4_host(pr.src[1]);
-    if (nf4 && pr.out != CT_BF16) return hipErrorInvalidValue;
+    // NF4 operands with fp32 output: split partials of the fast 256 x 256 runner only.
+    if (nf4 && pr.out != CT_BF16 && !(pr.out == CT_F32 && tile == TILE_256 && fast_ok(pr)))
+        return hipErrorInvalidValue;
     switch (CT_LAYOUT(pr.src[0], pr.src[1], pr.src[2], pr.src[3])) {
         case CT_LAYOUT(SRC_KC, SRC_KC, SRC_KC, SRC_KC):
             return launch_vec_out<SRC_KC, SRC_KC, SRC_KC, SRC_KC>(pr, tile, s);
@@ -1112,8 +1170,12 @@ hipError_t run(Problem &pr, hipStream_t s) {
         // NF4 loaders keep their own alignment (checked by nf4_fusable); VEC covers the
         // dense operands and the output.
         case CT_LAYOUT(SRC_KC, SRC_NF4, SRC_KC, SRC_KC):
+            if (pr.out == CT_F32)
+                return launch_cfg_fast<SRC_KC, SRC_NF4, SRC_KC, SRC_KC, CT_F32, TILE_256>(pr.p, pr.splits, s);
             return launch_mode<SRC_KC, SRC_NF4, SRC_KC, SRC_KC, CT_BF16>(pr, tile, s);
         case CT_LAYOUT(SRC_KC, SRC_NF4T, SRC_KC, SRC_KS):
+            if (pr.out == CT_F32)
+                return launch_cfg_fast<SRC_KC, SRC_NF4T, SRC_KC, SRC_KS, CT_F32, TILE_256>(pr.p, pr.splits, s);
             return launch_mode<SRC_KC, SRC_NF4T, SRC_KC, SRC_KS, CT_BF16>(pr, tile, s);
         default:
             return hipErrorInvalidValue;
@@ -1185,23 +1247,27 @@ hipError_t run_reduction(Problem pr, void *out, int64_t ldo, int add, void *ws, 
     pr.vec = pr.vec && aligned16(ws) && p.n % 8 == 0;
     hipError_t e = run(pr, s);
     if (e != hipSuccess) return e;
-    const int64_t count = p.m * p.n;
-    const unsigned grid = (unsigned)cdiv(count, 256);
+    const dim3 grid((unsigned)cdiv(p.n, 256), (unsigned)p.m);
     if (final_out == CT_F32)
         reduce_splits<CT_F32><<<grid, 256, 0, s>>>(static_cast<float *>(ws), splits, p.split_stride, p.m, p.n,
-                                                   out, ldo, add);
+                                                   out, ldo, add, nullptr);
     else
         reduce_splits<CT_BF16><<<grid, 256, 0, s>>>(static_cast<float *>(ws), splits, p.split_stride, p.m,
-                                                    p.n, out, ldo, add);
+                                                    p.n, out, ldo, add, nullptr);
     return hipGetLastError();
 }
 
 int to_status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
 
-// Workspace a few-row problem can use (0 when it takes the tiled kernels). Only the
-// shapes and source kinds matter, so the operands need not exist yet.
+// Workspace a problem can use for split partials: few rows (the skinny kernels) or the
+// rows between them and kMaterializeRows (mid_splits). Only the shapes and source kinds
+// matter, so the operands need not exist yet.
 int64_t problem_workspace(int64_t m, int64_t n, const int64_t k[2], int nseg, const int src_b[2]) {
-    if (m < 1 || m > 64 || n < 1) return 0;
+    if (m > 64) {
+        const int s = mid_splits(m, n, k[0] + (nseg > 1 ? k[1] : 0));
+        return s > 1 ? (int64_t)s * m * n * 4 : 0;
+    }
+    if (m < 1 || n < 1) return 0;
     GemmParams p{};
     p.m = m;
     p.n = n;
@@ -1341,15 +1407,16 @@ extern "C" int ct_gemm(const void *a, int64_t lda, int32_t trans_a, const void *
 
 namespace ct {
 namespace {
-#ifndef CT_MATERIALIZE_ROWS
-#define CT_MATERIALIZE_ROWS 512
-#endif
-// An NF4 base weight is decoded inside the GEMM's operand loader only while the rows are
-// few: each 256-row tile decodes its slice of the weight again, and from kMaterializeRows
-// rows on one ct_nf4_dequant pass into the workspace (the reference's materialize) plus
-// the dense GEMM is faster. Both give identical results.
-constexpr int64_t kMaterializeRows = CT_MATERIALIZE_ROWS;
-bool materialize_nf4(const ct_nf4_weight *w, int64_t m) { return w && m >= kMaterializeRows; }
+// Also decoded first: a weight without double quantization (the fast runner's NF4 loader
+// needs the nested state) in a problem that splits its reduction, so that it takes the
+// same kernel and summation order as the bf16 weight it decodes to.
+bool materialize_nf4(const ct_nf4_weight *w, int64_t m, int64_t n_out, int64_t ktot) {
+    return w && (m >= kMaterializeRows || (!w->nested && mid_splits(m, n_out, ktot) > 1));
+}
+// Workspace queries: nf4 is 0 (bf16 weight), 1 (NF4, double-quantized) or 2 (NF4, plain).
+bool materialize_kind(int32_t nf4, int64_t m, int64_t n_out, int64_t ktot) {
+    return nf4 && (m >= kMaterializeRows || (nf4 == 2 && mid_splits(m, n_out, ktot) > 1));
+}
 int64_t weight_bytes(int64_t n, int64_t k) { return (n * k * 2 + 255) & ~int64_t{255}; }
 
 // Splits the workspace into the materialized bf16 weight and the remainder.
@@ -1370,7 +1437,7 @@ extern "C" int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, 
     const int sb[2] = {SRC_NF4, SRC_KC};  // the dense weight (KC) has the same split shape
     const int64_t main = problem_workspace(m, n, ks, r > 0 ? 2 : 1, sb);
     const int64_t rest = inner > main ? inner : main;  // the two launches run in order on one stream
-    return (nf4 && m >= kMaterializeRows) ? weight_bytes(n, k) + rest : rest;
+    return materialize_kind(nf4, m, n, k + r) ? weight_bytes(n, k) + rest : rest;
 }
 
 extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense, const ct_nf4_weight *w_nf4,
@@ -1385,7 +1452,7 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
         const int st = validate_nf4(w_nf4);
         if (st) return st;
         if (w_nf4->rows != n || w_nf4->cols != k) return -CT_EINVAL_SHAPE;
-        if (materialize_nf4(w_nf4, m)) {
+        if (materialize_nf4(w_nf4, m, n, k + r)) {
             void *wbuf = nullptr;
             const int ws = take_weight(workspace, workspace_bytes, n, k, wbuf);
             if (ws) return ws;
@@ -1444,7 +1511,7 @@ extern "C" int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, 
     const int64_t main = problem_workspace(m, k, ks, r > 0 ? 2 : 1, sb);
     const int64_t rest = inner > main ? inner : main;
     // Many rows: the decoded weight (transposed) and the transposed factor a come first.
-    return (nf4 && m >= kMaterializeRows) ? weight_bytes(n, k) + weight_bytes(r, k) + rest : rest;
+    return materialize_kind(nf4, m, k, n + r) ? weight_bytes(n, k) + weight_bytes(r, k) + rest : rest;
 }
 
 extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_dense, const ct_nf4_weight *w_nf4,
@@ -1460,7 +1527,7 @@ extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_den
         const int st = validate_nf4(w_nf4);
         if (st) return st;
         if (w_nf4->rows != n || w_nf4->cols != k) return -CT_EINVAL_SHAPE;
-        if (materialize_nf4(w_nf4, m)) {
+        if (materialize_nf4(w_nf4, m, k, n + r)) {
             void *wbuf = nullptr;
             const int ws = take_weight(workspace, workspace_bytes, n, k, wbuf);
             if (ws) return ws;

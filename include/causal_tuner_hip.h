@@ -131,9 +131,12 @@ int ct_nf4_fused_supported(const ct_nf4_weight *w);
  * workspace (the reference's materialize) and the dense GEMM follows; below that the
  * weight is decoded tile by tile into LDS inside the GEMM (materialize fused away, which
  * needs ct_nf4_fused_supported(w_nf4), else -CT_EINVAL_LAYOUT). Both paths give results
- * bit-identical to ct_nf4_dequant's bf16 weight in the dense GEMM.
+ * bit-identical to ct_nf4_dequant's bf16 weight in the dense GEMM. Between 65 and 511
+ * rows the reduction may be split across workgroups (fp32 partials in the workspace,
+ * added in a fixed order); a weight without double quantization is then decoded first.
  * x [m, k] (ldx), a bf16 [r, k], b bf16 [n, r], bias bf16 [n] or null, out [m, n] (ldo),
- * xa bf16 [m, r] contiguous. The workspace query takes nf4 = 1 for an NF4 weight.
+ * xa bf16 [m, r] contiguous. The workspace query takes nf4 = 0 for a bf16 weight, 1 for
+ * a double-quantized NF4 weight and 2 for NF4 with plain absmax.
  */
 int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, int64_t r, int32_t nf4);
 int ct_forward_linear(const void *x, int64_t ldx,
@@ -149,7 +152,8 @@ int ct_forward_linear(const void *x, int64_t ldx,
  *   dx  = bf16(dy w + low a (+ dx if add))           [m, k]
  * dy [m, n] (lddy), w as in ct_forward_linear (a fused NF4 weight is decoded into LDS in
  * the transposed layout this product needs), a bf16 [r, k], b bf16 [n, r], dx [m, k]
- * (lddx), low bf16 [m, r] contiguous.
+ * (lddx), low bf16 [m, r] contiguous. Workspace query and row regimes as for
+ * ct_forward_linear.
  */
 int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, int64_t r, int32_t nf4);
 int ct_input_gradient(const void *dy, int64_t lddy,
