@@ -17,6 +17,8 @@ kernels   the same per-family breakdown for every timed family.
 dequant   C2: standalone NF4 dequant, GB/s against the 8 TB/s HBM peak.
 projections  C1 and C5: one projection fwd+bwd at several row counts, with the bound that
           applies (HBM for few rows, bf16 MFMA for many).
+skinny    C5 at 16 and 64 rows: the few-row forward and dx GEMM kernels alone, GB/s of their
+          algorithmic bytes against the HBM peak (--skinny-only runs just this leg).
 cpu_baseline  the reference's op sequence on the host CPU (oracle/lora.py), bounded sample.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-dequant] [--no-sweep]
@@ -263,7 +265,9 @@ def pmc_summary(fetch_csv, write_csv, family, mib):
     WRITE_SIZE, KiB per dispatch), each scaled by the same counter's reading for the copy
     probe of `mib` MiB; written to profiles/<family>_traffic.json."""
     # Forward and dx share the instantiation: the figure averages both families' launches.
-    patterns = {"dx_gemm": "gemm_big8<0, 0, 0, 0, 2>", "fwd_gemm": "gemm_big8<0, 0, 0, 0, 2>"}
+    # The few-row kernels (bench.py --skinny-only): both C5 shapes move the same weight bytes.
+    patterns = {"dx_gemm": "gemm_big8<0, 0, 0, 0, 2>", "fwd_gemm": "gemm_big8<0, 0, 0, 0, 2>",
+                "skinny_fwd": "rows_kernel<2, 0,", "skinny_dx": "cols_kernel<3, 1,"}
     copy_bytes = mib << 20
 
     def read(path, counter):
@@ -294,6 +298,64 @@ def pmc_summary(fetch_csv, write_csv, family, mib):
     print(json.dumps(out))
 
 
+def skinny_measure(device, shapes=((6144, 24576), (24576, 6144)), rows_list=(16, 64), copies=4, iters=40,
+                   rank=R):
+    """C5 few-row kernels alone: the forward GEMM of ct_forward_linear (x w^T + xa b^T on the
+    packed NF4 weight, with its split reduction) and the dx GEMM of ct_input_gradient
+    (dy w + low a), each timed with HIP events around its launches (ct_profile_*), over
+    `copies` weights used in rotation (> 256 MB, so the Infinity Cache cannot hold them).
+    Algorithmic bytes per launch: the packed weight and its scales, the rank-r factor
+    (bf16), the activations read and the output written once."""
+    from causal_tuner.kernels import _native
+    from causal_tuner.kernels.linear import _forward, _input_gradient
+    from causal_tuner.quant.nf4 import quantize_nf4
+    results = {}
+    for k, n in shapes:
+        g = torch.Generator(device=device).manual_seed(7)
+        weights = []
+        for _ in range(copies):
+            w = (torch.randn(n, k, device=device, generator=g) * 0.02).to(torch.bfloat16)
+            weights.append(quantize_nf4(w))
+            del w
+        a = (torch.randn(rank, k, device=device, generator=g) * 0.02).to(torch.bfloat16)
+        b = (torch.randn(n, rank, device=device, generator=g) * 0.01).to(torch.bfloat16)
+        nf4 = n * k * (0.5 + 1 / 64 + 1 / 4096)
+        for m in rows_list:
+            x = torch.randn(m, k, device=device, generator=g).to(torch.bfloat16)
+            dy = torch.randn(m, n, device=device, generator=g).to(torch.bfloat16)
+            out = torch.empty(m, n, device=device, dtype=torch.bfloat16)
+            xa = torch.empty(m, rank, device=device, dtype=torch.bfloat16)
+            dx = torch.empty(m, k, device=device, dtype=torch.bfloat16)
+            low = torch.empty(m, rank, device=device, dtype=torch.bfloat16)
+            for i in range(2 * copies):   # warm-up
+                packed, state = weights[i % copies]
+                _forward(x, packed, state, a, b, None, out, xa)
+                _input_gradient(dy, packed, state, a, b, dx, low, False)
+            torch.cuda.synchronize()
+            entry = {}
+            for key, slot, call, nbytes in (
+                    ("fwd", _native.CT_PROF_FWD_GEMM, lambda p, st: _forward(x, p, st, a, b, None, out, xa),
+                     nf4 + 2 * (n * rank + m * k + m * rank + m * n)),
+                    ("dx", _native.CT_PROF_DX_GEMM, lambda p, st: _input_gradient(dy, p, st, a, b, dx, low, False),
+                     nf4 + 2 * (rank * k + m * n + m * rank + m * k))):
+                with _native.KernelTimer(slot, capacity=iters + 8) as timer:
+                    for i in range(iters):
+                        call(*weights[i % copies])
+                    torch.cuda.synchronize()
+                    ms, launches, _ = timer.read(slot)
+                us = ms * 1e3 / max(launches, 1)
+                gbs = nbytes / (us * 1e-6) / 1e9
+                entry[key] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                              "bytes": int(nbytes)}
+            results[f"{k}->{n} M{m}"] = entry
+            log(f"  skinny {k}->{n} M={m:3d}: fwd {entry['fwd']['us']:7.1f} us {entry['fwd']['GB/s']:7.1f} GB/s"
+                f" | dx {entry['dx']['us']:7.1f} us {entry['dx']['GB/s']:7.1f} GB/s")
+            del x, dy, out, xa, dx, low
+        del weights, a, b
+        torch.cuda.empty_cache()
+    return results
+
+
 def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--pmc-summary":
         pmc_summary(sys.argv[2], sys.argv[3], sys.argv[4], int(sys.argv[5]))
@@ -305,6 +367,8 @@ def main():
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--no-dequant", action="store_true", help="skip the standalone dequant leg")
     parser.add_argument("--no-sweep", action="store_true", help="skip the C1/C5 projection legs")
+    parser.add_argument("--skinny-only", action="store_true",
+                        help="run only the C5 few-row kernel leg and print its JSON")
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MiB",
                         help="first run a plain device copy of this size (scales PMC byte counters)")
     args = parser.parse_args()
@@ -320,6 +384,9 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     if args.copy_probe:
         copy_probe(args.copy_probe)
+    if args.skinny_only:
+        print(json.dumps({"skinny": skinny_measure(device)}), flush=True)
+        return
 
     log("building C3 layer (NF4 quantization of seven projections)...")
     modules, inputs, grads = build_layer(device)
@@ -371,6 +438,10 @@ def main():
         log("C1 and C5 projections (fwd+bwd, NF4 base, one projection):")
         sweep = {"C1": projection_measure(device, [(1024, 1024)], [512], rank=16),
                  "C5": projection_measure(device, [(6144, 24576), (24576, 6144)], [16, 64, 256, 16384], iters=10)}
+    skinny = None
+    if not args.no_sweep:
+        log("C5 few-row kernels (M 16 and 64, weights rotated past the Infinity Cache):")
+        skinny = skinny_measure(device)
     cpu = None if args.no_cpu else cpu_baseline()
     log(f"cpu baseline: {cpu}")
 
@@ -392,6 +463,9 @@ def main():
         "projections": {"workload": "C1 (M 512, 1024->1024, rank 16) and C5 (6144<->24576, M 16..16384, rank "
                                     "256): one NF4-LoRA projection fwd+bwd through project_group + autograd",
                         "results": sweep},
+        "skinny": {"workload": "C5 M 16 and 64: the forward and dx GEMM kernels alone on the packed NF4 weight "
+                               "(split reduction included), four weight copies in rotation",
+                   "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "results": skinny},
     }
     print(json.dumps(line), flush=True)
 

@@ -495,7 +495,13 @@ __global__ __launch_bounds__(kSkThreads, SHARED ? cols_per_cu(MB) : (MB == 1 ? 2
         lcode2[tid] = p.code2[tid];
         __syncthreads();
     }
-    const int64_t j0 = (int64_t)blockIdx.x * kTCols;
+    // Column blocks 2q and 2q + 1 share every 128-byte line of a packed weight row (64
+    // bytes each). Workgroups are dealt to the eight XCDs round-robin by their linear id,
+    // so when the grid allows, ids x and x + 8 (one XCD) take blocks 2q and 2q + 1 and
+    // that XCD's L2 serves the second half of each line instead of a second fetch.
+    int bx = blockIdx.x;
+    if ((gridDim.x & 15) == 0) bx = (bx & ~15) | ((bx & 7) << 1) | ((bx >> 3) & 1);
+    const int64_t j0 = (int64_t)bx * kTCols;
     f32x4 acc[MB][8];
 #pragma unroll
     for (int mi = 0; mi < MB; ++mi)
