@@ -109,9 +109,12 @@ def time_events(fn, iters, warmup=3):
 def dequant_measure(device):
     """C2: standalone NF4 dequant of [28672, 8192] (and [8192, 8192]) to bf16, HBM GB/s.
 
-    Each launch is timed with HIP events around the kernel (ct_profile_*); the byte count
-    per launch is the decoder's algorithmic traffic (packed + scales + code books read,
-    bf16 output written). Several copies rotate when one would fit the 256 MB Infinity Cache."""
+    30 launches run back to back between one pair of HIP events on the stream (GB/s, frac;
+    rocprofv3's kernel durations agree, profiles/c2_dequant_kernel_stats.md); the same
+    launches with an event pair around each (ct_profile_*) are `per_launch_events`, about
+    2 us per launch slower on the 31 us shape. The byte count per launch is the decoder's
+    algorithmic traffic (packed + scales + code books read, bf16 output written). Several
+    copies rotate when one would fit the 256 MB Infinity Cache."""
     from causal_tuner.kernels import _native
     from causal_tuner.kernels.nf4_cuda import dequantize_nf4_into
     from causal_tuner.quant.nf4 import quantize_nf4
@@ -137,9 +140,23 @@ def dequant_measure(device):
             ms_total, launches, work = timer.read(_native.CT_PROF_DEQUANT)
         ms = ms_total / launches
         gbs = work / launches / (ms * 1e-3) / 1e9
-        results[f"{rows}x{cols}"] = {"GB/s": round(gbs, 1), "avg_us": round(ms * 1e3, 2), "bytes": int(moved),
-                                     "frac": round(gbs / HBM_PEAK_GBS, 4), "launches": launches,
-                                     "copies": copies}
+        # The same 30 launches back to back between one pair of events: the stream's decode
+        # throughput without an event pair around every launch.
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(30):
+            packed, state, out = weights[i % copies]
+            dequantize_nf4_into(packed, state, out)
+        stop.record()
+        stop.synchronize()
+        ms_stream = start.elapsed_time(stop) / 30
+        stream_gbs = moved / (ms_stream * 1e-3) / 1e9
+        results[f"{rows}x{cols}"] = {"GB/s": round(stream_gbs, 1), "avg_us": round(ms_stream * 1e3, 2),
+                                     "frac": round(stream_gbs / HBM_PEAK_GBS, 4), "bytes": int(moved),
+                                     "launches": 30, "copies": copies,
+                                     "per_launch_events": {"GB/s": round(gbs, 1), "avg_us": round(ms * 1e3, 2),
+                                                           "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                                           "launches": launches}}
         del weights
     return results
 
@@ -367,6 +384,8 @@ def main():
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--no-dequant", action="store_true", help="skip the standalone dequant leg")
     parser.add_argument("--no-sweep", action="store_true", help="skip the C1/C5 projection legs")
+    parser.add_argument("--dequant-only", action="store_true",
+                        help="run only the C2 standalone dequant leg and print its JSON")
     parser.add_argument("--skinny-only", action="store_true",
                         help="run only the C5 few-row kernel leg and print its JSON")
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MiB",
@@ -384,6 +403,9 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     if args.copy_probe:
         copy_probe(args.copy_probe)
+    if args.dequant_only:
+        print(json.dumps({"dequant": dequant_measure(device)}), flush=True)
+        return
     if args.skinny_only:
         print(json.dumps({"skinny": skinny_measure(device)}), flush=True)
         return
