@@ -53,6 +53,8 @@ _SIGNATURES = {
     "ct_accumulate_workspace": (_I64, [_I64, _I64, _I64]),
     "ct_silu_multiply": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P]),
     "ct_rope": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P]),
+    "ct_nf4_quantize_workspace": (_I64, [_I64, _I32, _I32]),
+    "ct_nf4_quantize": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "ct_profile_begin": (ctypes.c_int, [_I32, _I32]),
     "ct_profile_read": (ctypes.c_int, [_I32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64),
                                        ctypes.POINTER(ctypes.c_double)]),

@@ -4,8 +4,8 @@ The reference quantizes its frozen base weights through bitsandbytes>=0.45,<1
 (`pyproject.toml:21`) with `Params4bit(..., compress_statistics=True, quant_type="nf4")`
 (`modeling/lora.py:50-55`) and reads back the QuantState fields listed in `QuantState`
 below (`kernels/nf4_cuda.py:33-41`, `kernels/linear.py:8`). bitsandbytes is not a
-dependency here: `quantize_nf4` restates its published blockwise algorithm with torch
-tensor ops that run on the weight's device:
+dependency here: `quantize_nf4` restates its published blockwise algorithm, on the device
+with the HIP kernels of csrc/nf4_quantize.hip and on the host with torch tensor ops:
 
 1. absmax[g] = max |w| over each block of `blocksize` elements (zero-padded tail);
 2. x = w * (1 / absmax[g]) in fp32, NF4 code = number of code-book midpoints below x
@@ -137,9 +137,57 @@ def quantize_blockwise(values, code, blocksize=256):
 
 
 def quantize_nf4(weight, blocksize=64, compress_statistics=True):
-    """Quantize `weight` to NF4 on its device. Returns (packed uint8 [ceil(N/2), 1], QuantState)."""
+    """Quantize `weight` to NF4 on its device. Returns (packed uint8 [ceil(N/2), 1], QuantState).
+
+    Device tensors run the HIP quantizer (ct_nf4_quantize); host tensors run the same
+    algorithm as torch tensor ops (`_quantize_nf4_ops`)."""
     if blocksize < 2 or blocksize & (blocksize - 1):
         raise ValueError("NF4 blocksize must be a power of two >= 2")
+    if weight.is_cuda:
+        return _quantize_nf4_device(weight, blocksize, compress_statistics)
+    return _quantize_nf4_ops(weight, blocksize, compress_statistics)
+
+
+def _quantize_nf4_device(weight, blocksize, compress_statistics):
+    from ..kernels import _native
+    source = weight.detach()
+    if source.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"NF4 quantization of {source.dtype} weights is not supported")
+    flat = source.reshape(-1).contiguous()
+    device = flat.device
+    n = flat.numel()
+    nb = -(-n // blocksize) if n else 0
+    packed = torch.empty((n + 1) // 2, 1, dtype=torch.uint8, device=device)
+    code = nf4_code(device)
+    midpoints = nf4_thresholds(device)
+    nested = bool(compress_statistics)
+    lib = _native.library()
+    if nested:
+        code2 = dynamic_map().to(device)
+        absmax = torch.empty(nb, dtype=torch.uint8, device=device)
+        absmax2 = torch.empty(-(-nb // 256), dtype=torch.float32, device=device)
+        offset = torch.empty((), dtype=torch.float32, device=device)
+    else:
+        code2 = absmax2 = offset = None
+        absmax = torch.empty(nb, dtype=torch.float32, device=device)
+    ws_bytes = lib.ct_nf4_quantize_workspace(n, blocksize, int(nested))
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        status = lib.ct_nf4_quantize(
+            _native.ptr(flat), _native.dtype_code(flat.dtype), n, blocksize, int(nested), _native.ptr(midpoints),
+            _native.ptr(code2), _native.ptr(packed), _native.ptr(absmax), _native.ptr(absmax2), _native.ptr(offset),
+            _native.ptr(workspace), ws_bytes, _native.stream_of(flat))
+    _native.check(status, "ct_nf4_quantize")
+    if nested:
+        state2 = QuantState(absmax2, torch.Size([nb]), code2, 256, "dynamic", torch.float32)
+        state = QuantState(absmax, source.shape, code, blocksize, "nf4", source.dtype, offset, state2)
+    else:
+        state = QuantState(absmax, source.shape, code, blocksize, "nf4", source.dtype)
+    return packed, state
+
+
+def _quantize_nf4_ops(weight, blocksize=64, compress_statistics=True):
+    """The quantizer as torch tensor ops (host tensors)."""
     source = weight.detach()
     device = source.device
     flat = source.reshape(-1).float()

@@ -17,6 +17,7 @@
  * Reference interfaces (RealJosephus/causal-tuner, paths under src/causal_tuner/):
  *   kernels/nf4_cuda.py:9-43    _decode / dequantize_nf4   -> ct_nf4_dequant
  *   kernels/linear.py:6-13      materialize                -> ct_nf4_dequant
+ *   modeling/lora.py:50-55      bitsandbytes quantize_4bit -> ct_nf4_quantize
  *   kernels/linear.py:16-24     accumulate                 -> ct_accumulate
  *   kernels/linear.py:27-33     forward_linear             -> ct_forward_linear
  *   kernels/linear.py:36-39     input_gradient             -> ct_input_gradient
@@ -90,6 +91,26 @@ const char *ct_status_string(int status);
  * separately rounded add) when nested, else s[g] = absmax[g]. Bit-exact to the reference.
  */
 int ct_nf4_dequant(const ct_nf4_weight *w, void *out, int32_t out_dtype, hipStream_t stream);
+
+/*
+ * Replaces bitsandbytes' quantize_4bit(quant_type="nf4", compress_statistics=nested) as the
+ * reference calls it through Params4bit in Projection.install_nf4 (modeling/lora.py:50-55).
+ * w: n values of w_dtype (bf16, f16, f32), quantized in blocks of `blocksize` (a power of
+ * two) over the flat order: absmax[g] = max |w| of block g; codes = first of the 15
+ * `midpoints` (fp32, between the 16 NF4 code values) >= w * (1 / absmax[g]), NaN -> 15;
+ * packed[j] = code[2j] << 4 | code[2j + 1] (ceil(n / 2) bytes, 4-byte aligned, a zero pad
+ * nibble for odd n). nested = 0: absmax is fp32 [nb]. nested = 1: offset[0] = fp32 of the
+ * float64 mean of the fp32 absmax, absmax - offset is block-quantized in blocks of 256
+ * against code2 (the 256-entry signed dynamic map, bitsandbytes' binary search and
+ * midpoint rule): absmax is u8 [nb], absmax2 fp32 [ceil(nb / 256)]. The workspace holds the
+ * fp32 first-level absmax when nested. Finite inputs assumed (a NaN is not propagated into
+ * absmax).
+ */
+int64_t ct_nf4_quantize_workspace(int64_t n, int32_t blocksize, int32_t nested);
+int ct_nf4_quantize(const void *w, int32_t w_dtype, int64_t n, int32_t blocksize, int32_t nested,
+                    const float *midpoints, const float *code2, uint8_t *packed, void *absmax,
+                    float *absmax2, float *offset, void *workspace, int64_t workspace_bytes,
+                    hipStream_t stream);
 
 /*
  * Replaces the torch.mm / torch.addmm calls of the projection path (kernels/linear.py:28-33,

@@ -136,3 +136,56 @@ def test_full_size_dequant_matches_plain_c_oracle(shape):
     # the dequantized weight approximates the source within the NF4 grid resolution
     err = (got.float() - w.float()).abs().max().item()
     assert err <= 0.2 * w.float().abs().max().item()
+
+
+def _oracle_quantize(values, blocksize, nested):
+    return onf4.quantize(values.float().cpu().numpy(), blocksize=blocksize, nested=nested,
+                         storage=NAMES[values.dtype])
+
+
+@pytest.mark.parametrize("shape,blocksize,nested,dtype", [
+    ((71, 96), 64, True, torch.bfloat16), ((17, 19), 64, True, torch.bfloat16), ((300, 1000), 64, True, torch.bfloat16),
+    ((64, 64), 32, True, torch.float16), ((128, 96), 128, False, torch.float32), ((40, 100), 4096, True, torch.float32),
+    ((3, 5), 2, True, torch.bfloat16), ((1, 1), 64, False, torch.bfloat16)])
+def test_device_quantizer_matches_oracle(shape, blocksize, nested, dtype):
+    """ct_nf4_quantize (Projection.install_nf4's quantizer on the device) against the CPU
+    restatement of bitsandbytes' algorithm (oracle/nf4.py quantize), byte for byte: packed
+    codes, first-level absmax (u8 codes or fp32), absmax2 and offset. Odd element counts,
+    a 256-block group boundary (300 x 1000 = 4688 blocks), an all-zero block, blocksizes 2
+    to 4096 and every source dtype. Parity with bitsandbytes' own bytes stays unpinned
+    (bitsandbytes is absent and the reference's tests store no quantized bytes)."""
+    from causal_tuner.quant.nf4 import quantize_nf4
+    g = torch.Generator().manual_seed(sum(shape) + blocksize)
+    values = (torch.randn(*shape, generator=g) * 0.02).to(dtype)
+    if values.numel() >= 2 * blocksize:
+        values.view(-1)[blocksize:2 * blocksize] = 0   # an all-zero block (absmax 0, NaN codes)
+    packed, state = quantize_nf4(values.cuda(), blocksize=blocksize, compress_statistics=nested)
+    torch.cuda.synchronize()
+    want_packed, want = _oracle_quantize(values, blocksize, nested)
+    np.testing.assert_array_equal(packed.cpu().numpy().reshape(-1), want_packed)
+    np.testing.assert_array_equal(state.absmax.cpu().numpy(), want["absmax"])
+    assert state.blocksize == blocksize and state.dtype == dtype and tuple(state.shape) == shape
+    if nested:
+        assert np.float32(state.offset.item()) == want["offset"]
+        np.testing.assert_array_equal(state.state2.absmax.cpu().numpy(), want["absmax2"])
+        np.testing.assert_array_equal(state.state2.code.cpu().numpy(), want["code2"])
+    # and the host path (torch ops) agrees with the device path
+    hp, hs = quantize_nf4(values, blocksize=blocksize, compress_statistics=nested)
+    assert torch.equal(hp, packed.cpu()) and torch.equal(hs.absmax, state.absmax.cpu())
+
+
+def test_device_quantizer_round_trip_large():
+    """A C5-sized weight (24576 x 6144): quantize on the device, decode with ct_nf4_dequant,
+    and every element lands on its block's nearest code (|w - decoded| <= half the largest
+    code gap times the block's scale)."""
+    from causal_tuner.kernels.linear import materialize
+    from causal_tuner.quant.nf4 import quantize_nf4
+    g = torch.Generator(device="cuda").manual_seed(11)
+    w = (torch.randn(24576, 6144, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    packed, state = quantize_nf4(w)
+    back = materialize(packed, state, torch.float32)
+    err = (w.float() - back).abs().view(-1, 64).amax(1)
+    scale = w.float().abs().view(-1, 64).amax(1)
+    gap = float((torch.tensor(onf4.NF4_CODE[1:]) - torch.tensor(onf4.NF4_CODE[:-1])).max())
+    # the decoded scale differs from absmax by the 8-bit second level: allow 2% of it
+    assert bool((err <= scale * (gap / 2 + 0.02)).all())
