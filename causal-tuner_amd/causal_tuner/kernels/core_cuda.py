@@ -1,5 +1,11 @@
-"""Partial GPT-J rotary embedding on gfx950 (the rotary part of the reference's
+"""Row-wise RMS normalization and partial GPT-J rotary embedding on gfx950 (the reference's
 kernels/core_cuda.py).
+
+`RMS` (core_cuda.py:96-130) is the autograd function behind the decoder's RMSNorm: the HIP
+kernels ct_rms_forward / ct_rms_backward with the reference's rounding points, its
+private-gradient reuse (the input gradient written over the incoming gradient) and its
+output reconstruction mode (the backward reads the output and the weight instead of x).
+
 
 Same operator API as the reference: `rotate_owned_qk` (core_cuda.py:192-200) rotates the
 q and k outputs of a projection group in place, `inverse_rope_tile` (203-208) writes the
@@ -12,6 +18,52 @@ then the sum or difference rounded again).
 import torch
 
 from . import _native
+
+
+class RMS(torch.autograd.Function):
+    """y = T(T(x * rstd) * T(weight)) over the last dimension (reference core_cuda.py:96-130)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps, reuse_grad=False, reconstruct=False):
+        # Reconstruction and private-gradient reuse belong to frozen pre-norms.
+        ctx.reuse_grad = reuse_grad and not weight.requires_grad
+        ctx.reconstruct = reconstruct and not weight.requires_grad
+        if not (x.is_cuda and weight.is_cuda):
+            raise ValueError("RMS expects device tensors")
+        x = x.contiguous()
+        output = torch.empty_like(x)
+        width = x.shape[-1]
+        inverse = torch.empty(x.numel() // width if width else 0, device=x.device, dtype=torch.float32)
+        with torch.cuda.device(x.device):
+            status = _native.library().ct_rms_forward(
+                _native.ptr(x), _native.dtype_code(x.dtype), _native.ptr(weight.contiguous()),
+                _native.dtype_code(weight.dtype), _native.ptr(output), _native.ptr(inverse), len(inverse), width,
+                float(eps), _native.stream_of(x))
+        _native.check(status, "ct_rms_forward")
+        ctx.save_for_backward(output if ctx.reconstruct else x, weight, inverse)
+        return output
+
+    @staticmethod
+    def backward(ctx, grad):
+        x, weight, inverse = ctx.saved_tensors
+        grad = grad.contiguous()
+        # Only decoder pre-norms followed by analytic projections opt in: those projections
+        # hand back a private, freshly allocated input gradient.
+        result = (grad if ctx.reuse_grad else torch.empty_like(x)) if ctx.needs_input_grad[0] else None
+        dw = torch.empty_like(weight) if ctx.needs_input_grad[1] else None
+        width, rows = x.shape[-1], len(inverse)
+        lib = _native.library()
+        ws_bytes = lib.ct_rms_backward_workspace(rows, width, int(dw is not None))
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+        if result is not None or dw is not None:
+            with torch.cuda.device(x.device):
+                status = lib.ct_rms_backward(
+                    _native.ptr(x), _native.dtype_code(x.dtype), _native.ptr(weight.contiguous()),
+                    _native.dtype_code(weight.dtype), _native.ptr(inverse), _native.ptr(grad), _native.ptr(result),
+                    _native.ptr(dw), rows, width, int(ctx.reconstruct), _native.ptr(workspace), ws_bytes,
+                    _native.stream_of(x))
+            _native.check(status, "ct_rms_backward")
+        return (result, dw, None, None, None)[:len(ctx.needs_input_grad)]
 
 
 def _rope(x, y, cosine, sine, head_dim, *, inverse, rotated_only):

@@ -1343,6 +1343,15 @@ bool lowrank_split(int64_t m, int64_t n, int64_t k, int *tile, int *splits) {
     if (n > 256 || m < 4096 || k < 2048) return false;
     *tile = TILE_128;
     *splits = 4;
+#ifdef CT_TUNING
+    if (const char *env = getenv("CT_LOWRANK")) {
+        int t = 0, sp = 0;
+        if (sscanf(env, "%d,%d", &t, &sp) == 2) {
+            *tile = t;
+            *splits = sp;
+        }
+    }
+#endif
     return true;
 }
 }  // namespace

@@ -25,6 +25,7 @@
  *   kernels/linear.py:84,125    torch.mm(x, a.T, out=xa)   -> ct_gemm (NT, bf16 out)
  *   kernels/linear.py:124,167   torch.mm(dy, b, out=low)   -> ct_gemm (NN, bf16 out)
  *   kernels/mlp_cuda.py:10-35   _activation (SiLU x up)    -> ct_silu_multiply
+ *   kernels/core_cuda.py:29-130 RMS (_rms_forward/backward)  -> ct_rms_forward, ct_rms_backward
  *   kernels/core_cuda.py:133-229 _rope / _owned_qk_rope     -> ct_rope
  *                               (PartialRoPE, inverse_rope_tile, rotate_owned_qk)
  */
@@ -141,6 +142,27 @@ int ct_gemm(const void *a, int64_t lda, int32_t trans_a,
  * its GEMMs always read a materialised weight.
  */
 int ct_nf4_fused_supported(const ct_nf4_weight *w);
+
+/*
+ * Replace _rms_forward / _rms_backward / _rms_weight_reduce behind RMS
+ * (kernels/core_cuda.py:29-130; the decoder's RMSNorm, modeling/model.py:38-64).
+ * x, y [rows, width] of x_dtype (contiguous), w [width] of w_dtype, rstd fp32 [rows].
+ *   forward:  rstd = 1 / sqrt(sum(x^2) / width + eps);  y = T(T(x * rstd) * T(w)),
+ *             T = rounding to x_dtype.
+ *   backward: g = T(go * T(w)); with from_output = 0, x is the input and
+ *             gx = rstd * (g - x * (rstd^2 * sum(g * x) / width)); with from_output = 1,
+ *             x is the forward's output y and n = y / T(w), gx = rstd * (g - n * sum(g * n) / width).
+ *             dw = sum over rows of go * T(x * rstd) in fp32, rounded to w_dtype (needs
+ *             from_output = 0 and the workspace of ct_rms_backward_workspace).
+ * go and gx are of x_dtype; gx may be go itself (written in place), either of gx and dw
+ * may be null. Deterministic: fixed reduction orders.
+ */
+int ct_rms_forward(const void *x, int32_t x_dtype, const void *w, int32_t w_dtype, void *y, float *rstd,
+                   int64_t rows, int64_t width, float eps, hipStream_t stream);
+int64_t ct_rms_backward_workspace(int64_t rows, int64_t width, int32_t weight_grad);
+int ct_rms_backward(const void *x, int32_t x_dtype, const void *w, int32_t w_dtype, const float *rstd,
+                    const void *go, void *gx, void *dw, int64_t rows, int64_t width, int32_t from_output,
+                    void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * Replaces forward_linear (kernels/linear.py:27-33):

@@ -16,5 +16,7 @@ Contents (each function cites the reference file:line it restates):
                   down projections, analytic backward) in float64.
   rope.py         the partial GPT-J rotary embedding with its per-product rounding
                   (numpy float32 + explicit round-to-nearest-even).
+  rmsnorm.py      row-wise RMS normalization forward/backward (float64 with the
+                  reference's rounding points to the activation dtype).
   nf4_dequant.c   plain-C decode, the timed CPU baseline (built by oracle/Makefile).
 """
