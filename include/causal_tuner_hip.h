@@ -26,6 +26,7 @@
  *   kernels/linear.py:124,167   torch.mm(dy, b, out=low)   -> ct_gemm (NN, bf16 out)
  *   kernels/mlp_cuda.py:10-35   _activation (SiLU x up)    -> ct_silu_multiply
  *   kernels/core_cuda.py:29-130 RMS (_rms_forward/backward)  -> ct_rms_forward, ct_rms_backward
+ *   kernels/loss_cuda.py:11-70  weighted_ce (_statistics)   -> ct_weighted_ce
  *   kernels/core_cuda.py:133-229 _rope / _owned_qk_rope     -> ct_rope
  *                               (PartialRoPE, inverse_rope_tile, rotate_owned_qk)
  */
@@ -163,6 +164,19 @@ int64_t ct_rms_backward_workspace(int64_t rows, int64_t width, int32_t weight_gr
 int ct_rms_backward(const void *x, int32_t x_dtype, const void *w, int32_t w_dtype, const float *rstd,
                     const void *go, void *gx, void *dw, int64_t rows, int64_t width, int32_t from_output,
                     void *workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Replaces weighted_ce (kernels/loss_cuda.py:11-70: _statistics, _finish), the fused
+ * weighted cross-entropy of the chunked projection loss. logits [rows, vocab] of dtype
+ * (row pitch ld), targets int64 [rows], weights fp32 [rows], loss fp32 [rows]:
+ *   lse[r] = log sum_c exp(logits[r, c]);  loss[r] = weights[r] * (lse[r] - logits[r, target[r]])
+ * (the target term is 0 for a target outside [0, vocab)). With gradient != 0 the logits
+ * are overwritten with (exp(logits - lse) - onehot(target)) * weights[r], rounded to dtype.
+ * Deterministic (fixed reduction order).
+ */
+int ct_weighted_ce(void *logits, int32_t dtype, int64_t rows, int64_t vocab, int64_t ld,
+                   const int64_t *targets, const float *weights, float *loss, int32_t gradient,
+                   hipStream_t stream);
 
 /*
  * Replaces forward_linear (kernels/linear.py:27-33):
