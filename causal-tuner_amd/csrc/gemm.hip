@@ -845,9 +845,24 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
             } else {
                 uint16_t *c = static_cast<uint16_t *>(p.c) + row * p.ldc + out_shift + col;
                 if (p.beta) {
+                    if (VEC && full && (FN == 8 || FN == 4)) {
+                        // one 16- or 8-byte read of the FN existing values
+                        uint32_t w[FN / 2];
+                        if constexpr (FN == 8) {
+                            const uint4 q = *reinterpret_cast<const uint4 *>(c);
+                            w[0] = q.x, w[1] = q.y, w[2] = q.z, w[3] = q.w;
+                        } else {
+                            const uint2 q = *reinterpret_cast<const uint2 *>(c);
+                            w[0] = q.x, w[1] = q.y;
+                        }
 #pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        if (full || col + j < ncols) v[j] = v[j] + bf16_to_f32(c[j]);
+                        for (int j = 0; j < FN; ++j)
+                            v[j] = v[j] + bf16_to_f32((uint16_t)(j & 1 ? w[j / 2] >> 16 : w[j / 2] & 0xffffu));
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < FN; ++j)
+                            if (full || col + j < ncols) v[j] = v[j] + bf16_to_f32(c[j]);
+                    }
                 }
                 if (VEC && full && FN >= 2) {
                     uint32_t w[FN / 2];
