@@ -15,7 +15,9 @@ lib/libcausal_tuner_hip.so:
   bit-identical; add=False ignores the destination's contents).
 
 The bf16 path is the device path. CPU tensors keep the reference's torch semantics (its
-unfused CPU route); device tensors of another compute dtype raise NotImplementedError.
+unfused CPU route); device tensors of another compute dtype raise NotImplementedError,
+except in `accumulate`, which keeps the reference's addmm for operands that are not bf16
+(the fp32 projection loss uses it; linear.py:22-24).
 """
 
 import torch
@@ -121,8 +123,6 @@ def accumulate(output, left, right, *, add=True):
         _native.check(status, "ct_accumulate")
         if target.buffer is not output:
             output.copy_(target.buffer + output if add else target.buffer)
-    elif left.is_cuda:
-        _unsupported("accumulate", output, left, right)
     elif output.dtype != left.dtype:
         output.addmm_(left.to(output.dtype), right.to(output.dtype), beta=beta)
     else:

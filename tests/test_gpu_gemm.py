@@ -68,9 +68,8 @@ def test_gemm_layouts_and_tails(m, n, k, trans_a, trans_b, out):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_gradient_first_write_ignores_uninitialized_storage(dtype):
-    """tests/test_kernel_workspaces.py:269-279 (accumulate with add=False ignores NaN)."""
-    if dtype != torch.bfloat16:
-        pytest.skip("the HIP accumulate computes bf16 products (fp32 operands are not on the device path)")
+    """tests/test_kernel_workspaces.py:269-279 (accumulate with add=False ignores NaN). bf16
+    operands run ct_accumulate; fp32 operands keep the reference's addmm (linear.py:22-24)."""
     from causal_tuner.kernels.linear import accumulate
     left = torch.randn(19, 37, device="cuda", dtype=dtype)
     right = torch.randn(37, 23, device="cuda", dtype=dtype)
