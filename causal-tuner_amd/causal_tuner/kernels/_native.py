@@ -59,6 +59,8 @@ _SIGNATURES = {
     "ct_rms_backward_workspace": (_I64, [_I64, _I64, _I32]),
     "ct_rms_backward": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _P, _P, _P, _I64, _I64, _I32, _P, _I64, _P]),
     "ct_weighted_ce": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _P, _P, _P, _I32, _P]),
+    "ct_adamw_step": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _I32, ctypes.c_double, ctypes.c_double,
+                                     ctypes.c_double, ctypes.c_double, ctypes.c_double, _I32, _I32, _P]),
     "ct_profile_begin": (ctypes.c_int, [_I32, _I32]),
     "ct_profile_read": (ctypes.c_int, [_I32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64),
                                        ctypes.POINTER(ctypes.c_double)]),

@@ -27,6 +27,7 @@
  *   kernels/mlp_cuda.py:10-35   _activation (SiLU x up)    -> ct_silu_multiply
  *   kernels/core_cuda.py:29-130 RMS (_rms_forward/backward)  -> ct_rms_forward, ct_rms_backward
  *   kernels/loss_cuda.py:11-70  weighted_ce (_statistics)   -> ct_weighted_ce
+ *   training/engine.py:10-16    torch fused AdamW step      -> ct_adamw_step
  *   kernels/core_cuda.py:133-229 _rope / _owned_qk_rope     -> ct_rope
  *                               (PartialRoPE, inverse_rope_tile, rotate_owned_qk)
  */
@@ -177,6 +178,31 @@ int ct_rms_backward(const void *x, int32_t x_dtype, const void *w, int32_t w_dty
 int ct_weighted_ce(void *logits, int32_t dtype, int64_t rows, int64_t vocab, int64_t ld,
                    const int64_t *targets, const float *weights, float *loss, int32_t gradient,
                    hipStream_t stream);
+
+/*
+ * Replaces the optimizer step of torch.optim.AdamW(fused=True) as the reference builds it
+ * (training/engine.py:10-16; amsgrad off): one launch updates every tensor of a parameter
+ * group. `tensors` (device memory) lists `count` parameters; each has a fp32 step counter
+ * on the device, and its gradient and states in the parameter's dtype (CT_F32 or CT_BF16
+ * for all of them). `chunks` (device memory) holds n_chunks pairs (tensor index, first
+ * element); a workgroup updates chunk_elems elements from there (fewer at a tensor's end).
+ * With count_step != 0 every step counter is first incremented by one. Per element, with
+ * s = *step: p -= lr * weight_decay * p; m = beta1 m + (1 - beta1) g;
+ * v = beta2 v + (1 - beta2) g^2; p -= lr / (1 - beta1^s) * m / (sqrt(v) / sqrt(1 - beta2^s) + eps)
+ * (g negated when maximize). Tensors must not overlap.
+ */
+typedef struct ct_adamw_tensor {
+    void *param;
+    const void *grad;
+    void *exp_avg;
+    void *exp_avg_sq;
+    const float *step;
+    int64_t numel;
+} ct_adamw_tensor;
+
+int ct_adamw_step(const ct_adamw_tensor *tensors, int64_t count, const int64_t *chunks, int64_t n_chunks,
+                  int64_t chunk_elems, int32_t dtype, double lr, double beta1, double beta2, double eps,
+                  double weight_decay, int32_t maximize, int32_t count_step, hipStream_t stream);
 
 /*
  * Replaces forward_linear (kernels/linear.py:27-33):
