@@ -21,6 +21,8 @@ projections  C1 and C5: one projection fwd+bwd at several row counts, with the b
           applies (HBM for few rows, bf16 MFMA for many).
 skinny    C5 at 16 and 64 rows: the few-row forward and dx GEMM kernels alone, GB/s of their
           algorithmic bytes against the HBM peak (--skinny-only runs just this leg).
+c4        C4: tokens/s of a full LoRA training step of the 24-layer decoder on 4096 packed
+          tokens (modeling/decoder.py, FusedAdamW; --c4-only runs just this leg).
 cpu_baseline  the reference's op sequence on the host CPU (oracle/lora.py), bounded sample.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-dequant] [--no-sweep]
@@ -375,6 +377,66 @@ def skinny_measure(device, shapes=((6144, 24576), (24576, 6144)), rows_list=(16,
     return results
 
 
+def c4_measure(device, steps=5, warmup=2):
+    """C4: one full LoRA training step of the 24-layer MQA decoder (d 2048, 16 x 128 query
+    heads, one KV head, I 8192, vocab 49152, partial RoPE theta 1e4, NF4 frozen bases, rank
+    256 LoRA on all seven projections) on 4096 packed tokens in 4 records of random lengths:
+    forward, projection loss, backward, gradient clipping and the FusedAdamW step. Tokens/s
+    over `steps` steps after `warmup`."""
+    from causal_tuner.modeling.decoder import Decoder, DecoderConfig
+    from causal_tuner.optim import FusedAdamW
+    config = DecoderConfig()
+    seq = 4096
+    torch.manual_seed(6)
+    model = Decoder(config, rank=256, device=device)
+    for name, p in model.named_parameters():
+        if "lora_B" in name:
+            torch.nn.init.normal_(p, std=0.01)
+    model.install_nf4()
+    torch.cuda.empty_cache()
+    g = torch.Generator().manual_seed(6)
+    cuts = sorted(torch.randperm(seq - 1, generator=g)[:3].add(1).tolist())
+    bounds = [0, *cuts, seq]
+    records = [(bounds[i], bounds[i + 1]) for i in range(4)]
+    ids = torch.randint(config.vocab_size, (1, seq), generator=g).to(device)
+    targets = torch.roll(ids, -1, dims=1)
+    weights = torch.ones(1, seq, device=device)
+    for _, stop in records:
+        weights[0, stop - 1] = 0
+    params = [p for p in model.parameters() if p.requires_grad]
+    opt = FusedAdamW([{"params": [p for p in params if p.ndim > 1], "weight_decay": 0.0}], lr=1e-4,
+                     betas=(0.9, 0.999), eps=1e-8)
+
+    def step():
+        loss = model.loss(ids, targets, weights, records)
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(params, 1.0, foreach=True)
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    ms = elapsed * 1e3 / steps
+    result = {"workload": "C4: 24-layer MQA decoder LoRA training step (d 2048, 16x128 q heads, 1 KV head, "
+                          "I 8192, V 49152, rank 256 on all 7 projections, NF4 frozen bases), 4096 packed "
+                          "tokens in 4 records, projection loss, clip, FusedAdamW",
+              "records": [b - a for a, b in records], "tokens_per_s": round(seq / (ms * 1e-3), 1),
+              "ms_per_step": round(ms, 3), "steps": steps, "warmup": warmup,
+              "trainable_params": sum(p.numel() for p in params), "loss": round(float(loss.detach()), 4),
+              "attention": "torch SDPA (flash backend), causal per record",
+              "peak_mem_GiB": round(torch.cuda.max_memory_allocated() / 2**30, 2)}
+    del model, opt, params
+    torch.cuda.empty_cache()
+    return result
+
+
 def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--pmc-summary":
         pmc_summary(sys.argv[2], sys.argv[3], sys.argv[4], int(sys.argv[5]))
@@ -390,6 +452,8 @@ def main():
                         help="run only the C2 standalone dequant leg and print its JSON")
     parser.add_argument("--skinny-only", action="store_true",
                         help="run only the C5 few-row kernel leg and print its JSON")
+    parser.add_argument("--no-c4", action="store_true", help="skip the C4 training-step leg")
+    parser.add_argument("--c4-only", action="store_true", help="run only the C4 training-step leg")
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MiB",
                         help="first run a plain device copy of this size (scales PMC byte counters)")
     args = parser.parse_args()
@@ -410,6 +474,9 @@ def main():
         return
     if args.skinny_only:
         print(json.dumps({"skinny": skinny_measure(device)}), flush=True)
+        return
+    if args.c4_only:
+        print(json.dumps({"c4": c4_measure(device)}), flush=True)
         return
 
     log("building C3 layer (NF4 quantization of seven projections)...")
@@ -478,6 +545,11 @@ def main():
     if not args.no_sweep:
         log("C5 few-row kernels (M 16 and 64, weights rotated past the Infinity Cache):")
         skinny = skinny_measure(device)
+    c4 = None
+    if not args.no_c4:
+        log("C4 training step (24 layers, 4096 tokens):")
+        c4 = c4_measure(device)
+        log(f"  {c4['tokens_per_s']} tokens/s, {c4['ms_per_step']} ms per step")
     cpu = None if args.no_cpu else cpu_baseline()
     log(f"cpu baseline: {cpu}")
 
@@ -502,6 +574,7 @@ def main():
         "skinny": {"workload": "C5 M 16 and 64: the forward and dx GEMM kernels alone on the packed NF4 weight "
                                "(split reduction included), four weight copies in rotation",
                    "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "results": skinny},
+        "c4": c4,
     }
     print(json.dumps(line), flush=True)
 
