@@ -104,3 +104,37 @@ def test_unsupported_layouts_are_refused_not_miscomputed():
     xa = torch.empty(8, 4, device="cuda", dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="fused"):
         _forward(x, packed, state, a, b, None, out, xa)
+
+
+@pytest.mark.parametrize("m,k,n,r", [(4096, 2048, 2048, 256), (1024, 4096, 4096, 64), (4096, 8192, 2048, 256),
+                                     (2048, 2048, 640, 16)])
+def test_many_rows_with_less_than_one_round_of_large_tiles(m, k, n, r):
+    """Many rows whose output gives the 256 x 256 workgroups less than one round (the C4
+    shapes q/o/down at 4096 tokens take the 128 x 128 grid): forward and dx (also with
+    add=True) against fp32 products of the same bf16 operands rounded once, and a repeated
+    forward bit-identical."""
+    packed, state = _weight(n, k, seed=3)
+    dense = materialize(packed, state, torch.bfloat16)
+    x, a, b, dy, bias = _inputs(m, k, n, r, seed=2)
+    xf, wf, af, bf, dyf = (t.float() for t in (x, dense, a, b, dy))
+    out = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+    xa = torch.empty(m, r, device="cuda", dtype=torch.bfloat16)
+    _forward(x, packed, state, a, b, bias, out, xa)
+    want_xa = xf @ af.T
+    want_out = xf @ wf.T + bias.float() + xa.float() @ bf.T
+    dx = torch.full((m, k), float("nan"), device="cuda", dtype=torch.bfloat16)
+    low = torch.empty(m, r, device="cuda", dtype=torch.bfloat16)
+    _input_gradient(dy, packed, state, a, b, dx, low, False)
+    want_dx = dyf @ wf + low.float() @ af
+    def check(got, want, name, tol=1e-3):   # against the fp32 result rounded once to bf16
+        want = want.to(torch.bfloat16).float()
+        norm = ((got.float() - want).norm() / want.norm()).item()
+        assert norm <= tol, (name, norm)
+    for got, want, name in ((xa, want_xa, "xa"), (out, want_out, "out"), (dx, want_dx, "dx")):
+        check(got, want, name)
+    acc = dx.clone()
+    _input_gradient(dy, packed, state, a, b, acc, low, True)
+    check(acc, dx.float() + want_dx, "dx+=")
+    again = torch.empty_like(out)
+    _forward(x, packed, state, a, b, bias, again, torch.empty_like(xa))
+    assert torch.equal(again.view(torch.int16), out.view(torch.int16))
