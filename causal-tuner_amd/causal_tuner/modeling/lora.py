@@ -77,3 +77,15 @@ class Projection(nn.Module):
         from ..kernels.nf4_cuda import dequantize_nf4
         state = self.quantized.weight.quant_state
         return dequantize_nf4(self.quantized.weight.data, state, state.dtype)
+
+    def merged_weight(self, dtype=None):
+        """The tensor the reference's merged export writes for this projection
+        (checkpointing/io.py:270-280): the base weight (NF4 decoded by ct_nf4_dequant) plus
+        lora_B @ lora_A, summed in fp32 and rounded once to `dtype` (default: the base
+        weight's dtype)."""
+        with torch.no_grad():
+            weight = self.base_weight()
+            dtype = dtype or weight.dtype
+            if self.rank:
+                weight = weight.float() + self.lora_B.float() @ self.lora_A.float()
+            return weight.detach().to(dtype).contiguous()

@@ -284,3 +284,23 @@ def test_parameter_gradients_grouped_launch(m, n, k, r):
         if want.numel():
             _, norm = olora.relative_error(got.cpu(), want)
             assert norm <= 1e-5, (name, norm)
+
+
+@pytest.mark.parametrize("nf4", [False, True])
+def test_merged_weight_is_the_effective_linear_map(nf4):
+    """Projection.merged_weight (the merged export, reference checkpointing/io.py:270-280):
+    fp32 sum of the decoded base and lora_B @ lora_A, rounded once. Against a float64
+    host product rounded to bf16, and x @ merged^T against the projection's own forward."""
+    module = _projection(96, 40, 8, nf4=nf4, seed=3)
+    merged = module.merged_weight()
+    assert merged.dtype == torch.bfloat16 and merged.shape == (40, 96)
+    base = module.base_weight().double().cpu()
+    want = (base + module.lora_B.detach().double().cpu() @ module.lora_A.detach().double().cpu()).float()
+    diff = (merged.float().cpu() - want.bfloat16().float()).abs()
+    ulp = want.abs().clamp_min(2 ** -126) * 2 ** -7
+    assert bool((diff <= ulp).all())
+    x = torch.randn(16, 96, device="cuda").to(torch.bfloat16)
+    via_merged = x.float() @ merged.float().T
+    via_forward = module(x).float()
+    assert ((via_merged - via_forward).norm() / via_forward.norm()).item() <= 1e-2
+    assert module.merged_weight(torch.float32).dtype == torch.float32
