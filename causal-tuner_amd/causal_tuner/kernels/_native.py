@@ -15,6 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIBRARY = os.path.normpath(os.path.join(_HERE, "..", "..", "lib", "libcausal_tuner_hip.so"))
 
 CT_F32, CT_F16, CT_BF16 = 0, 1, 2
+CT_CAST_MAX = 16  # tensors per ct_cast_f32_bf16 call (include/causal_tuner_hip.h)
 CT_PROF_FWD_GEMM, CT_PROF_DX_GEMM, CT_PROF_DEQUANT, CT_PROF_PARAM, CT_PROF_LOWRANK = 1, 2, 4, 8, 16
 DTYPE_CODES = {torch.float32: CT_F32, torch.float16: CT_F16, torch.bfloat16: CT_BF16}
 
@@ -59,6 +60,7 @@ _SIGNATURES = {
     "ct_rms_backward_workspace": (_I64, [_I64, _I64, _I32]),
     "ct_rms_backward": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _P, _P, _P, _I64, _I64, _I32, _P, _I64, _P]),
     "ct_weighted_ce": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _P, _P, _P, _I32, _P]),
+    "ct_cast_f32_bf16": (ctypes.c_int, [_P, _P, _P, _I32, _P]),
     "ct_adamw_step": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _I32, ctypes.c_double, ctypes.c_double,
                                      ctypes.c_double, ctypes.c_double, ctypes.c_double, _I32, _I32, _P]),
     "ct_profile_begin": (ctypes.c_int, [_I32, _I32]),

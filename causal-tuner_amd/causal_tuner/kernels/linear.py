@@ -20,6 +20,8 @@ except in `accumulate`, which keeps the reference's addmm for operands that are 
 (the fp32 projection loss uses it; linear.py:22-24).
 """
 
+import ctypes
+
 import torch
 
 from . import _native
@@ -93,6 +95,36 @@ class _Contiguous(_Output):
 
 
 # ----------------------------------------------------------------------------- operators
+def cast_all(tensors, dtype):
+    """[t.to(dtype) for t in tensors], with the fp32 device tensors that go to bf16 rounded
+    in one launch (ct_cast_f32_bf16) into views of one buffer: the reference casts each
+    LoRA factor separately (kernels/linear.py:70,108; kernels/mlp_cuda.py:62,110)."""
+    out = [None] * len(tensors)
+    batch = [i for i, t in enumerate(tensors)
+             if dtype == torch.bfloat16 and t.dtype == torch.float32 and t.is_cuda and t.is_contiguous()
+             and t.numel()]
+    if len(batch) > 1:
+        lib = _native.library()
+        padded = [(tensors[i].numel() + 7) // 8 * 8 for i in batch]   # 16-byte aligned views
+        buffer = torch.empty(sum(padded), dtype=torch.bfloat16, device=tensors[batch[0]].device)
+        offset = 0
+        for i, size in zip(batch, padded):
+            out[i] = buffer[offset:offset + tensors[i].numel()].view(tensors[i].shape)
+            offset += size
+        limit = _native.CT_CAST_MAX
+        for first in range(0, len(batch), limit):
+            part = batch[first:first + limit]
+            src = (ctypes.c_void_p * len(part))(*[tensors[i].data_ptr() for i in part])
+            dst = (ctypes.c_void_p * len(part))(*[out[i].data_ptr() for i in part])
+            counts = (ctypes.c_int64 * len(part))(*[tensors[i].numel() for i in part])
+            with torch.cuda.device(buffer.device):
+                status = lib.ct_cast_f32_bf16(ctypes.cast(src, ctypes.c_void_p), ctypes.cast(dst, ctypes.c_void_p),
+                                              ctypes.cast(counts, ctypes.c_void_p), len(part),
+                                              _native.stream_of(buffer))
+            _native.check(status, "ct_cast_f32_bf16")
+    return [t.to(dtype) if o is None else o for t, o in zip(tensors, out)]
+
+
 def materialize(weight, state, dtype):
     if state is not None:
         if state.quant_type != "nf4":
@@ -291,9 +323,10 @@ class _LoRAGroup(torch.autograd.Function):
         outputs = []
         step = tile or max(len(flat), 1)
         rows = min(step, len(flat))
+        factors = cast_all([value for i in range(len(states)) for value in parameters[i*4+1:i*4+3]], dtype)
         for index, state in enumerate(states):
             weight, a, b, bias = parameters[index*4:index*4+4]
-            base, ac, bc = _Base(weight, state, dtype), a.to(dtype), b.to(dtype)
+            base, ac, bc = _Base(weight, state, dtype), factors[2*index], factors[2*index+1]
             bias = None if bias is None else bias.to(dtype)
             out = torch.empty((len(flat), base.rows), device=x.device, dtype=dtype)
             low = torch.empty((rows, len(a)), device=x.device, dtype=dtype)
@@ -302,6 +335,7 @@ class _LoRAGroup(torch.autograd.Function):
                 base.forward(part, ac, bc, bias, out[start:start+step], low[:len(part)])
             outputs.append(out.reshape(*x.shape[:-1], base.rows))
             del base, ac, bc, low
+        del factors
         if head_dim:
             from .core_cuda import rotate_owned_qk
             rotate_owned_qk(outputs[0], outputs[1], cosine, sine, head_dim)
@@ -321,10 +355,11 @@ class _LoRAGroup(torch.autograd.Function):
         rotary = (torch.empty(rows*max(len(b) for b in parameters[2:8:4]), device=x.device, dtype=ctx.dtype)
                   if ctx.head_dim else None)
         results = []
+        factors = cast_all([value for i in range(len(ctx.states)) for value in parameters[i*4+1:i*4+3]], ctx.dtype)
         for index, (state, grad) in enumerate(zip(ctx.states, grad_outputs)):
             weight, a, b, _ = parameters[index*4:index*4+4]
             base = _Base(weight, state, ctx.dtype) if dx is not None else None
-            ac, bc = a.to(ctx.dtype), b.to(ctx.dtype)
+            ac, bc = factors[2*index], factors[2*index+1]
             dy = grad.reshape(-1, grad.shape[-1]).to(ctx.dtype)
             allocate = torch.empty_like if len(flat) else torch.zeros_like
             da, db = allocate(a), allocate(b)

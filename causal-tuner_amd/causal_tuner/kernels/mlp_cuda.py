@@ -10,7 +10,7 @@ packed below 512 rows (the GEMMs decode it in LDS) and is decoded once per call 
 import torch
 
 from . import _native
-from .linear import _Base, forward_linear, input_gradient, parameter_gradients, projection_parameters, _low_rank
+from .linear import _Base, cast_all, forward_linear, input_gradient, parameter_gradients, projection_parameters, _low_rank
 
 
 def _silu(gate, up, h, dg, du, backward, reconstruct):
@@ -68,7 +68,8 @@ def _bases(parameters, states, dtype):
 def _forward_into(output, x, dtype, tile, states, parameters, residual, *, save=False):
     flat = x.reshape(-1, x.shape[-1]).to(dtype)
     matrices = _bases(parameters, states, dtype)
-    adapters = [(parameters[4*i+1].to(dtype), parameters[4*i+2].to(dtype)) for i in range(3)]
+    cast = cast_all([parameters[4*i+j] for i in range(3) for j in (1, 2)], dtype)
+    adapters = [(cast[2*i], cast[2*i+1]) for i in range(3)]
     rows = min(tile, len(flat))
     width = matrices[0].rows
     workspace = torch.empty((1 if save else 2, rows, width), device=x.device, dtype=dtype)
@@ -122,7 +123,8 @@ class _TiledLoRAMLP(torch.autograd.Function):
         grad = grad.reshape_as(flat).to(ctx.dtype)
         dx = torch.empty_like(flat) if ctx.needs_input_grad[0] else None
         matrices = _bases(parameters, ctx.states, ctx.dtype)
-        adapters = [(parameters[4*i+1].to(ctx.dtype), parameters[4*i+2].to(ctx.dtype)) for i in range(3)]
+        cast = cast_all([parameters[4*i+j] for i in range(3) for j in (1, 2)], ctx.dtype)
+        adapters = [(cast[2*i], cast[2*i+1]) for i in range(3)]
         allocate = torch.empty_like if len(flat) else torch.zeros_like
         gradients = [(allocate(parameters[4*i+1]), allocate(parameters[4*i+2])) for i in range(3)]
         rows = min(ctx.tile, len(flat))

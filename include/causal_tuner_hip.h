@@ -28,6 +28,7 @@
  *   kernels/core_cuda.py:29-130 RMS (_rms_forward/backward)  -> ct_rms_forward, ct_rms_backward
  *   kernels/loss_cuda.py:11-70  weighted_ce (_statistics)   -> ct_weighted_ce
  *   training/engine.py:10-16    torch fused AdamW step      -> ct_adamw_step
+ *   kernels/linear.py:70,108    a.to(dtype), b.to(dtype)    -> ct_cast_f32_bf16 (one launch per group)
  *   kernels/core_cuda.py:133-229 _rope / _owned_qk_rope     -> ct_rope
  *                               (PartialRoPE, inverse_rope_tile, rotate_owned_qk)
  */
@@ -191,6 +192,17 @@ int ct_weighted_ce(void *logits, int32_t dtype, int64_t rows, int64_t vocab, int
  * v = beta2 v + (1 - beta2) g^2; p -= lr / (1 - beta1^s) * m / (sqrt(v) / sqrt(1 - beta2^s) + eps)
  * (g negated when maximize). Tensors must not overlap.
  */
+/*
+ * Rounds `count` (at most CT_CAST_MAX) fp32 tensors to bf16 in one launch: dst[i][j] =
+ * bf16(src[i][j]) for j < counts[i], round to nearest even, as torch's .to(torch.bfloat16).
+ * Replaces the per-tensor casts of the LoRA factors a.to(dtype), b.to(dtype) in
+ * _LoRAGroup (kernels/linear.py:70,108) and _TiledLoRAMLP (kernels/mlp_cuda.py:62,110).
+ * src, dst and counts are host arrays of device pointers and sizes; tensors must not overlap.
+ */
+#define CT_CAST_MAX 16
+int ct_cast_f32_bf16(const float *const *src, uint16_t *const *dst, const int64_t *counts, int32_t count,
+                     hipStream_t stream);
+
 typedef struct ct_adamw_tensor {
     void *param;
     const void *grad;
