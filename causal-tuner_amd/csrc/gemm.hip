@@ -957,12 +957,12 @@ __global__ __launch_bounds__(256) void fill_zero(float *p, int64_t count) {
 // Sums the split partials of the grouped parameter-gradient GEMM, ws[z][i][c] with
 // c < width, in split order: columns below `gcols` are da[i][c] (c < k), the rest are
 // db[c - gcols][i] (< n), i.e. dB^T is written transposed.
+// Grid: (column blocks of 256, rows r); eight partials in flight per thread.
 __global__ __launch_bounds__(256) void reduce_param(const float *__restrict__ ws, int splits, int64_t stride,
                                                     int64_t r, int64_t width, int64_t gcols, int64_t k,
                                                     int64_t n, float *da, float *db, int add) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= r * width) return;
-    const int64_t i = idx / width, c = idx % width;
+    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x, i = blockIdx.y;
+    if (c >= width) return;
     float *o;
     if (c < gcols) {
         if (c >= k) return;
@@ -971,8 +971,16 @@ __global__ __launch_bounds__(256) void reduce_param(const float *__restrict__ ws
         if (c - gcols >= n) return;
         o = db + (c - gcols) * r + i;
     }
-    float s = ws[idx];
-    for (int z = 1; z < splits; ++z) s += ws[z * stride + idx];
+    const int64_t idx = i * width + c;
+    float s = 0.f;
+    for (int z0 = 0; z0 < splits; z0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = z0 + j < splits ? ws[(z0 + j) * stride + idx] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (z0 + j < splits) s = (z0 + j == 0) ? v[j] : s + v[j];
+    }
     *o = add ? s + *o : s;
 }
 
@@ -1761,7 +1769,7 @@ extern "C" int ct_parameter_gradients(const void *x, int64_t ldx, const void *dy
     hipError_t e = run(pr, stream);
     if (e == hipSuccess) {
         const int64_t gcols = k > 0 ? (int64_t)pl.gt * kTileEdge[pl.tile] : 0;
-        const unsigned grid = (unsigned)cdiv(r * pl.width, 256);
+        const dim3 grid((unsigned)cdiv(pl.width, 256), (unsigned)r);
         reduce_param<<<grid, 256, 0, stream>>>(static_cast<const float *>(workspace), pl.splits, r * pl.width, r,
                                                pl.width, gcols, k, n, da, db, add);
         e = hipGetLastError();
