@@ -44,13 +44,13 @@ _SIGNATURES = {
                                _P]),
     "ct_forward_linear_workspace": (_I64, [_I64, _I64, _I64, _I64, _I32]),
     "ct_forward_linear": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _P, _I64, _P,
-                                         _I64, _I64, _I64, _I64, _P, _I64, _P]),
+                                         _I64, _I32, _I64, _I64, _I64, _I64, _P, _I64, _P]),
     "ct_input_gradient_workspace": (_I64, [_I64, _I64, _I64, _I64, _I32]),
     "ct_input_gradient": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _I64, _P,
                                          _I64, _I64, _I64, _I64, _I32, _P, _I64, _P]),
     "ct_parameter_gradients_workspace": (_I64, [_I64, _I64, _I64, _I64]),
-    "ct_parameter_gradients": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32,
-                                              _P, _I64, _P]),
+    "ct_parameter_gradients": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64,
+                                              _I64, _I32, _P, _I64, _P]),
     "ct_accumulate_workspace": (_I64, [_I64, _I64, _I64]),
     "ct_silu_multiply": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P]),
     "ct_rope": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P]),

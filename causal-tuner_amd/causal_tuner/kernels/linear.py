@@ -95,34 +95,69 @@ class _Contiguous(_Output):
 
 
 # ----------------------------------------------------------------------------- operators
-def cast_all(tensors, dtype):
+def cast_all(tensors, dtype, outputs=None):
     """[t.to(dtype) for t in tensors], with the fp32 device tensors that go to bf16 rounded
-    in one launch (ct_cast_f32_bf16) into views of one buffer: the reference casts each
-    LoRA factor separately (kernels/linear.py:70,108; kernels/mlp_cuda.py:62,110)."""
+    in one launch (ct_cast_f32_bf16) into views of one buffer (or into the given contiguous
+    `outputs`, where an entry is not None): the reference casts each LoRA factor separately
+    (kernels/linear.py:70,108; kernels/mlp_cuda.py:62,110)."""
+    outputs = outputs or [None] * len(tensors)
     out = [None] * len(tensors)
     batch = [i for i, t in enumerate(tensors)
              if dtype == torch.bfloat16 and t.dtype == torch.float32 and t.is_cuda and t.is_contiguous()
              and t.numel()]
-    if len(batch) > 1:
+    if len(batch) > 1 or any(outputs[i] is not None for i in batch):
         lib = _native.library()
-        padded = [(tensors[i].numel() + 7) // 8 * 8 for i in batch]   # 16-byte aligned views
+        fresh = [i for i in batch if outputs[i] is None]
+        padded = [(tensors[i].numel() + 7) // 8 * 8 for i in fresh]   # 16-byte aligned views
         buffer = torch.empty(sum(padded), dtype=torch.bfloat16, device=tensors[batch[0]].device)
         offset = 0
-        for i, size in zip(batch, padded):
+        for i, size in zip(fresh, padded):
             out[i] = buffer[offset:offset + tensors[i].numel()].view(tensors[i].shape)
             offset += size
+        for i in batch:
+            if outputs[i] is not None:
+                out[i] = outputs[i]
         limit = _native.CT_CAST_MAX
         for first in range(0, len(batch), limit):
             part = batch[first:first + limit]
             src = (ctypes.c_void_p * len(part))(*[tensors[i].data_ptr() for i in part])
             dst = (ctypes.c_void_p * len(part))(*[out[i].data_ptr() for i in part])
             counts = (ctypes.c_int64 * len(part))(*[tensors[i].numel() for i in part])
-            with torch.cuda.device(buffer.device):
+            with torch.cuda.device(tensors[batch[0]].device):
                 status = lib.ct_cast_f32_bf16(ctypes.cast(src, ctypes.c_void_p), ctypes.cast(dst, ctypes.c_void_p),
                                               ctypes.cast(counts, ctypes.c_void_p), len(part),
-                                              _native.stream_of(buffer))
+                                              _native.stream_of(tensors[batch[0]]))
             _native.check(status, "ct_cast_f32_bf16")
-    return [t.to(dtype) if o is None else o for t, o in zip(tensors, out)]
+    result = [t.to(dtype) if o is None else o for t, o in zip(tensors, out)]
+    for i, o in enumerate(outputs):
+        if o is not None and result[i] is not o:
+            o.copy_(result[i])
+            result[i] = o
+    return result
+
+
+def group_factors(parameters, count, dtype, x):
+    """The compute-dtype LoRA factors of a projection group, cast together, and for a group
+    whose projections share rank and input on the device the stacked [a_1; a_2; ...]
+    (count * r rows) that gives every projection's xa in one GEMM. Returns (factors,
+    stacked or None) with factors = [a_1, b_1, a_2, b_2, ...]."""
+    tensors = [value for i in range(count) for value in parameters[i*4+1:i*4+3]]
+    ranks = {len(tensors[2*i]) for i in range(count)}
+    stack = None
+    if (count > 1 and x.is_cuda and dtype == torch.bfloat16 and len(ranks) == 1 and ranks != {0}
+            and len({tensors[2*i].shape[1] for i in range(count)}) == 1):
+        r = ranks.pop()
+        stack = torch.empty((count * r, tensors[0].shape[1]), dtype=dtype, device=x.device)
+        outputs = [stack[i*r:(i+1)*r] if j == 0 else None for i in range(count) for j in (0, 1)]
+        return cast_all(tensors, dtype, outputs), stack
+    return cast_all(tensors, dtype), stack
+
+
+def _shared_xa(flat, stack):
+    """x [a_1; a_2; ...]^T for a group: one ct_gemm, column slice i is projection i's xa."""
+    xa = torch.empty((len(flat), len(stack)), dtype=flat.dtype, device=flat.device)
+    _low_rank(flat, stack, xa, transpose=True)
+    return xa
 
 
 def materialize(weight, state, dtype):
@@ -178,14 +213,18 @@ def forward_linear(x, weight, a, b, *, out, xa, bias=None):
     _forward(x, weight, None, a, b, bias, out, xa)
 
 
-def _forward(x, weight, state, a, b, bias, out, xa):
+def _forward(x, weight, state, a, b, bias, out, xa, xa_given=False):
+    """ct_forward_linear; with xa_given, xa (a row-major view, e.g. a column slice of a
+    group's shared x [a_1; a_2; ...]^T) already holds x a^T and is only read."""
     m, k = x.shape
     n, r = out.shape[1], a.shape[0]
     x, ldx = _rows(x)
     w = None if weight is None else weight.contiguous()
     a, b = a.contiguous(), b.contiguous()
     bias = None if bias is None else bias.contiguous()
-    target, low = _Output(out), _Contiguous(xa)
+    target, low = _Output(out), _Output(xa)
+    if xa_given and low.buffer is not xa:
+        low.buffer.copy_(xa)
     desc = None if state is None else _native.nf4_descriptor(w, state)
     lib = _native.library()
     ws = _workspace(lib.ct_forward_linear_workspace(m, n, k, r, _native.nf4_kind(desc)), x.device)
@@ -193,10 +232,11 @@ def _forward(x, weight, state, a, b, bias, out, xa):
         status = lib.ct_forward_linear(
             _native.ptr(x), ldx, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),
             _native.ptr(b), _native.ptr(bias), _native.ptr(target.buffer), target.ld, _native.ptr(low.buffer),
-            m, n, k, r, _native.ptr(ws), ws.numel(), _native.stream_of(x))
+            low.ld, int(bool(xa_given)), m, n, k, r, _native.ptr(ws), ws.numel(), _native.stream_of(x))
     _native.check(status, "ct_forward_linear")
     target.finish()
-    low.finish()
+    if not xa_given:
+        low.finish()
 
 
 def input_gradient(dy, weight, a, b, dx, low, *, add=False):
@@ -248,7 +288,8 @@ def parameter_gradients(x, dy, da, db, low, xa, *, add):
     n, r = dy.shape[1], low.shape[1]
     x, ldx = _rows(x)
     dy, lddy = _rows(dy)
-    low, xa = low.contiguous(), xa.contiguous()
+    low, ldlow = _rows(low)
+    xa, ldxa = _rows(xa)
     if not (da.is_contiguous() and db.is_contiguous()):
         accumulate(da, low.T, x, add=add)
         accumulate(db, dy.T, xa, add=add)
@@ -256,8 +297,8 @@ def parameter_gradients(x, dy, da, db, low, xa, *, add):
     lib = _native.library()
     ws = _workspace(lib.ct_parameter_gradients_workspace(m, n, k, r), x.device)
     with torch.cuda.device(x.device):
-        status = lib.ct_parameter_gradients(_native.ptr(x), ldx, _native.ptr(dy), lddy, _native.ptr(low),
-                                             _native.ptr(xa), _native.ptr(da), _native.ptr(db), m, n, k, r,
+        status = lib.ct_parameter_gradients(_native.ptr(x), ldx, _native.ptr(dy), lddy, _native.ptr(low), ldlow,
+                                             _native.ptr(xa), ldxa, _native.ptr(da), _native.ptr(db), m, n, k, r,
                                              int(add), _native.ptr(ws), ws.numel(), _native.stream_of(x))
     _native.check(status, "ct_parameter_gradients")
 
@@ -295,8 +336,10 @@ class _Base:
             self.matrix = materialize(weight, state, dtype)
         self.rows = int(state.shape[0]) if state is not None else len(weight)
 
-    def forward(self, x, a, b, bias, out, xa):
-        if self.state is None:
+    def forward(self, x, a, b, bias, out, xa, xa_given=False):
+        if xa_given:   # device path only: xa holds x a^T already
+            _forward(x, self.matrix if self.state is None else self.weight, self.state, a, b, bias, out, xa, True)
+        elif self.state is None:
             forward_linear(x, self.matrix, a, b, bias=bias, out=out, xa=xa)
         else:
             _forward(x, self.weight, self.state, a, b, bias, out, xa)
@@ -323,19 +366,28 @@ class _LoRAGroup(torch.autograd.Function):
         outputs = []
         step = tile or max(len(flat), 1)
         rows = min(step, len(flat))
-        factors = cast_all([value for i in range(len(states)) for value in parameters[i*4+1:i*4+3]], dtype)
+        factors, stack = group_factors(parameters, len(states), dtype, x)
+        # One tile over all rows: the projections' xa come from one GEMM over the stacked
+        # factors (the same products; the fp32 sums may be split differently than in
+        # separate launches, so a value can differ by one bf16 rounding).
+        shared = _shared_xa(flat, stack) if stack is not None and 0 < len(flat) <= step else None
         for index, state in enumerate(states):
             weight, a, b, bias = parameters[index*4:index*4+4]
             base, ac, bc = _Base(weight, state, dtype), factors[2*index], factors[2*index+1]
             bias = None if bias is None else bias.to(dtype)
             out = torch.empty((len(flat), base.rows), device=x.device, dtype=dtype)
-            low = torch.empty((rows, len(a)), device=x.device, dtype=dtype)
-            for start in range(0, len(flat), step):
-                part = flat[start:start+step]
-                base.forward(part, ac, bc, bias, out[start:start+step], low[:len(part)])
+            if shared is not None:
+                r = len(a)
+                base.forward(flat, ac, bc, bias, out, shared[:, index*r:(index+1)*r], xa_given=True)
+            else:
+                low = torch.empty((rows, len(a)), device=x.device, dtype=dtype)
+                for start in range(0, len(flat), step):
+                    part = flat[start:start+step]
+                    base.forward(part, ac, bc, bias, out[start:start+step], low[:len(part)])
+                del low
             outputs.append(out.reshape(*x.shape[:-1], base.rows))
-            del base, ac, bc, low
-        del factors
+            del base, ac, bc
+        del factors, stack, shared
         if head_dim:
             from .core_cuda import rotate_owned_qk
             rotate_owned_qk(outputs[0], outputs[1], cosine, sine, head_dim)
@@ -355,7 +407,8 @@ class _LoRAGroup(torch.autograd.Function):
         rotary = (torch.empty(rows*max(len(b) for b in parameters[2:8:4]), device=x.device, dtype=ctx.dtype)
                   if ctx.head_dim else None)
         results = []
-        factors = cast_all([value for i in range(len(ctx.states)) for value in parameters[i*4+1:i*4+3]], ctx.dtype)
+        factors, stack = group_factors(parameters, len(ctx.states), ctx.dtype, x)
+        shared = _shared_xa(flat, stack) if stack is not None and 0 < len(flat) <= step else None
         for index, (state, grad) in enumerate(zip(ctx.states, grad_outputs)):
             weight, a, b, _ = parameters[index*4:index*4+4]
             base = _Base(weight, state, ctx.dtype) if dx is not None else None
@@ -364,7 +417,8 @@ class _LoRAGroup(torch.autograd.Function):
             allocate = torch.empty_like if len(flat) else torch.zeros_like
             da, db = allocate(a), allocate(b)
             low = torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype)
-            xa = torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype)
+            xa = (shared[:, index*len(a):(index+1)*len(a)] if shared is not None
+                  else torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype))
             rotate = ctx.head_dim and index < 2
             for start in range(0, len(flat), step):
                 stop = start+step
@@ -378,7 +432,8 @@ class _LoRAGroup(torch.autograd.Function):
                     base.input_gradient(signal, ac, bc, dx[start:stop], part_low, index > 0)
                 else:
                     _low_rank(signal, bc, part_low, transpose=False)
-                _low_rank(flat[start:stop], ac, part_xa, transpose=True)
+                if shared is None:
+                    _low_rank(flat[start:stop], ac, part_xa, transpose=True)
                 parameter_gradients(flat[start:stop], signal, da, db, part_low, part_xa, add=start > 0)
             results.extend((None, da, db, None))
             del base, ac, bc, dy

@@ -1340,7 +1340,7 @@ bool nf4_fusable(const ct_nf4_weight *w) {
 
 using namespace ct;
 
-extern "C" int ct_abi_version(void) { return 4; }
+extern "C" int ct_abi_version(void) { return 5; }
 
 extern "C" const char *ct_status_string(int status) {
     switch (status) {
@@ -1474,12 +1474,12 @@ extern "C" int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, 
 
 extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense, const ct_nf4_weight *w_nf4,
                                  const void *a, const void *b, const void *bias, void *out, int64_t ldo, void *xa,
-                                 int64_t m, int64_t n, int64_t k, int64_t r, void *workspace, int64_t workspace_bytes,
-                                 hipStream_t stream) {
+                                 int64_t ldxa, int32_t xa_given, int64_t m, int64_t n, int64_t k, int64_t r,
+                                 void *workspace, int64_t workspace_bytes, hipStream_t stream) {
     if (m < 0 || n < 0 || k < 0 || r < 0) return -CT_EINVAL_SHAPE;
     if (m == 0 || n == 0) return 0;
-    if (!x || !out || (!w_dense == !w_nf4) || (r > 0 && (!a || !b || !xa))) return -CT_EINVAL_POINTER;
-    if (ldx < k || ldo < n) return -CT_EINVAL_SHAPE;
+    if (!x || !out || (!w_dense == !w_nf4) || (r > 0 && (!b || !xa || (!xa_given && !a)))) return -CT_EINVAL_POINTER;
+    if (ldx < k || ldo < n || (r > 0 && ldxa < r)) return -CT_EINVAL_SHAPE;
     if (w_nf4) {
         const int st = validate_nf4(w_nf4);
         if (st) return st;
@@ -1496,11 +1496,11 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
             return -CT_EINVAL_LAYOUT;
         }
     }
-    if (r > 0) {
+    if (r > 0 && !xa_given) {
         // xa = x a^T  (NT, bf16 out)
         const int slot = profile_open(CT_PROF_LOWRANK, stream);
-        const int st = ct_gemm(x, ldx, 0, a, k, 1, xa, r, CT_BF16, nullptr, 0, m, r, k, workspace, workspace_bytes,
-                               stream);
+        const int st = ct_gemm(x, ldx, 0, a, k, 1, xa, ldxa, CT_BF16, nullptr, 0, m, r, k, workspace,
+                               workspace_bytes, stream);
         profile_close(slot, stream, 2.0 * m * r * k);
         if (st) return st;
     }
@@ -1508,7 +1508,7 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
     pr.p.seg[0].a = dense(x, ldx);
     pr.p.seg[0].b = w_nf4 ? nf4_operand(w_nf4) : dense(w_dense, k);
     pr.p.seg[0].k = k;
-    pr.p.seg[1].a = dense(xa, r);
+    pr.p.seg[1].a = dense(xa, ldxa);
     pr.p.seg[1].b = dense(b, r);
     pr.p.seg[1].k = r;
     pr.p.nseg = r > 0 ? 2 : 1;
@@ -1708,9 +1708,9 @@ extern "C" int64_t ct_parameter_gradients_workspace(int64_t m, int64_t n, int64_
 }
 
 extern "C" int ct_parameter_gradients(const void *x, int64_t ldx, const void *dy, int64_t lddy, const void *low,
-                                      const void *xa, float *da, float *db, int64_t m, int64_t n, int64_t k,
-                                      int64_t r, int32_t add, void *workspace, int64_t workspace_bytes,
-                                      hipStream_t stream) {
+                                      int64_t ldlow, const void *xa, int64_t ldxa, float *da, float *db, int64_t m,
+                                      int64_t n, int64_t k, int64_t r, int32_t add, void *workspace,
+                                      int64_t workspace_bytes, hipStream_t stream) {
     if (m < 0 || n < 0 || k < 0 || r < 0) return -CT_EINVAL_SHAPE;
     if (r == 0 || (n == 0 && k == 0)) return 0;
     if ((k > 0 && !da) || (n > 0 && !db)) return -CT_EINVAL_POINTER;
@@ -1721,13 +1721,13 @@ extern "C" int ct_parameter_gradients(const void *x, int64_t ldx, const void *dy
         return to_status(hipGetLastError());
     }
     if ((k > 0 && (!x || !low)) || (n > 0 && (!dy || !xa))) return -CT_EINVAL_POINTER;
-    if (ldx < k || lddy < n) return -CT_EINVAL_SHAPE;
+    if (ldx < k || lddy < n || ldlow < r || ldxa < r) return -CT_EINVAL_SHAPE;
     const ParamPlan pl = param_plan(m, n, k, r);
     if (!workspace || workspace_bytes < param_workspace(pl, r)) return -CT_EINVAL_WORKSPACE;
     const int slot = profile_open(CT_PROF_PARAM, stream);
     Problem pr{};
     // Group 0 (dA): A(i, t) = low[t][i], B(q, t) = x[t][q]; group 1 (dB^T): xa and dy.
-    Segment dA{dense(low, r), dense(x, ldx), m}, dB{dense(xa, r), dense(dy, lddy), m};
+    Segment dA{dense(low, ldlow), dense(x, ldx), m}, dB{dense(xa, ldxa), dense(dy, lddy), m};
     if (k > 0 && n > 0) {
         pr.p.seg[0] = dA;
         pr.p.seg[1] = dB;

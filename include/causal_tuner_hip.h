@@ -230,14 +230,17 @@ int ct_adamw_step(const ct_adamw_tensor *tensors, int64_t count, const int64_t *
  * rows the reduction may be split across workgroups (fp32 partials in the workspace,
  * added in a fixed order); a weight without double quantization is then decoded first.
  * x [m, k] (ldx), a bf16 [r, k], b bf16 [n, r], bias bf16 [n] or null, out [m, n] (ldo),
- * xa bf16 [m, r] contiguous. The workspace query takes nf4 = 0 for a bf16 weight, 1 for
- * a double-quantized NF4 weight and 2 for NF4 with plain absmax.
+ * xa bf16 [m, r] (row pitch ldxa >= r). With xa_given != 0, xa already holds x a^T (a may
+ * be null): projections that share x compute their xa together, x [a_1; a_2; ...]^T in
+ * one ct_gemm with ldxa = the summed ranks, and pass column slices. The workspace query
+ * takes nf4 = 0 for a bf16 weight, 1 for a double-quantized NF4 weight and 2 for NF4 with
+ * plain absmax.
  */
 int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, int64_t r, int32_t nf4);
 int ct_forward_linear(const void *x, int64_t ldx,
                       const void *w_dense, const ct_nf4_weight *w_nf4,
                       const void *a, const void *b, const void *bias,
-                      void *out, int64_t ldo, void *xa,
+                      void *out, int64_t ldo, void *xa, int64_t ldxa, int32_t xa_given,
                       int64_t m, int64_t n, int64_t k, int64_t r,
                       void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
@@ -263,13 +266,14 @@ int ct_input_gradient(const void *dy, int64_t lddy,
  * (kernels/linear.py:16-24):
  *   da = low^T x   (+ da if add)   float32 [r, k]
  *   db = dy^T xa   (+ db if add)   float32 [n, r]
- * x [m, k] (ldx), dy [m, n] (lddy), low and xa bf16 [m, r] contiguous. The m-reduction is
- * split over workgroups and summed in a fixed order, so repeated calls are bit-identical;
- * add = 0 never reads da/db (NaN-filled storage is ignored).
+ * x [m, k] (ldx), dy [m, n] (lddy), low bf16 [m, r] (ldlow), xa bf16 [m, r] (ldxa; a
+ * column slice of a group's shared xa). The m-reduction is split over workgroups and
+ * summed in a fixed order, so repeated calls are bit-identical; add = 0 never reads da/db
+ * (NaN-filled storage is ignored).
  */
 int64_t ct_parameter_gradients_workspace(int64_t m, int64_t n, int64_t k, int64_t r);
 int ct_parameter_gradients(const void *x, int64_t ldx, const void *dy, int64_t lddy,
-                           const void *low, const void *xa, float *da, float *db,
+                           const void *low, int64_t ldlow, const void *xa, int64_t ldxa, float *da, float *db,
                            int64_t m, int64_t n, int64_t k, int64_t r, int32_t add,
                            void *workspace, int64_t workspace_bytes, hipStream_t stream);
 

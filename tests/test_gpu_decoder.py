@@ -123,7 +123,7 @@ def test_decoder_adamw_step_lowers_the_loss():
     first = None
     for _ in range(3):
         loss = model.loss(ids[None], targets[None], weights[None], records, token_budget=16)
-        first = float(loss) if first is None else first
+        first = float(loss.detach()) if first is None else first
         loss.backward()
         torch.nn.utils.clip_grad_norm_(params, 1.0, foreach=True)
         opt.step()
