@@ -136,21 +136,21 @@ def cast_all(tensors, dtype, outputs=None):
     return result
 
 
-def group_factors(parameters, count, dtype, x):
-    """The compute-dtype LoRA factors of a projection group, cast together, and for a group
-    whose projections share rank and input on the device the stacked [a_1; a_2; ...]
-    (count * r rows) that gives every projection's xa in one GEMM. Returns (factors,
-    stacked or None) with factors = [a_1, b_1, a_2, b_2, ...]."""
+def group_factors(parameters, count, dtype, x, shared=None):
+    """The compute-dtype LoRA factors of `count` projections, cast together, and when the
+    first `shared` of them (default all) read the same input on the device with one rank,
+    the stacked [a_1; a_2; ...] (shared * r rows) that gives their xa in one GEMM.
+    Returns (factors, stacked or None) with factors = [a_1, b_1, a_2, b_2, ...]."""
+    shared = count if shared is None else shared
     tensors = [value for i in range(count) for value in parameters[i*4+1:i*4+3]]
-    ranks = {len(tensors[2*i]) for i in range(count)}
-    stack = None
-    if (count > 1 and x.is_cuda and dtype == torch.bfloat16 and len(ranks) == 1 and ranks != {0}
-            and len({tensors[2*i].shape[1] for i in range(count)}) == 1):
+    ranks = {len(tensors[2*i]) for i in range(shared)}
+    if (shared > 1 and x.is_cuda and dtype == torch.bfloat16 and len(ranks) == 1 and ranks != {0}
+            and len({tensors[2*i].shape[1] for i in range(shared)}) == 1):
         r = ranks.pop()
-        stack = torch.empty((count * r, tensors[0].shape[1]), dtype=dtype, device=x.device)
-        outputs = [stack[i*r:(i+1)*r] if j == 0 else None for i in range(count) for j in (0, 1)]
+        stack = torch.empty((shared * r, tensors[0].shape[1]), dtype=dtype, device=x.device)
+        outputs = [stack[i*r:(i+1)*r] if j == 0 and i < shared else None for i in range(count) for j in (0, 1)]
         return cast_all(tensors, dtype, outputs), stack
-    return cast_all(tensors, dtype), stack
+    return cast_all(tensors, dtype), None
 
 
 def _shared_xa(flat, stack):

@@ -10,7 +10,7 @@ packed below 512 rows (the GEMMs decode it in LDS) and is decoded once per call 
 import torch
 
 from . import _native
-from .linear import _Base, cast_all, forward_linear, input_gradient, parameter_gradients, projection_parameters, _low_rank
+from .linear import _Base, group_factors, forward_linear, input_gradient, parameter_gradients, projection_parameters, _low_rank
 
 
 def _silu(gate, up, h, dg, du, backward, reconstruct):
@@ -68,15 +68,24 @@ def _bases(parameters, states, dtype):
 def _forward_into(output, x, dtype, tile, states, parameters, residual, *, save=False):
     flat = x.reshape(-1, x.shape[-1]).to(dtype)
     matrices = _bases(parameters, states, dtype)
-    cast = cast_all([parameters[4*i+j] for i in range(3) for j in (1, 2)], dtype)
+    cast, stack = group_factors(parameters, 3, dtype, flat, shared=2)
     adapters = [(cast[2*i], cast[2*i+1]) for i in range(3)]
     rows = min(tile, len(flat))
     width = matrices[0].rows
     workspace = torch.empty((1 if save else 2, rows, width), device=x.device, dtype=dtype)
     low = torch.empty((rows, max(len(a) for a, _ in adapters)), device=x.device, dtype=dtype)
+    r = len(adapters[0][0])
+    # gate and up read the same rows: with a shared rank their xa come from one GEMM over
+    # [a_gate; a_up] into the two column halves of one buffer.
+    pair = None if stack is None or save else torch.empty((rows, 2 * r), device=x.device, dtype=dtype)
+    if save:
+        if stack is not None:
+            both = torch.empty((len(flat), 2 * r), device=x.device, dtype=dtype)
+            held = (both[:, :r], both[:, r:])
+        else:
+            held = tuple(torch.empty((len(flat), len(a)), device=x.device, dtype=dtype) for a, _ in adapters[:2])
     saved = (() if not save else (
-        *(torch.empty((len(flat), width), device=x.device, dtype=dtype) for _ in range(2)),
-        *(torch.empty((len(flat), len(a)), device=x.device, dtype=dtype) for a, _ in adapters[:2])))
+        *(torch.empty((len(flat), width), device=x.device, dtype=dtype) for _ in range(2)), *held))
     destination = output.view_as(flat)
     for start in range(0, len(flat), tile):
         part = flat[start:start+tile]
@@ -85,13 +94,28 @@ def _forward_into(output, x, dtype, tile, states, parameters, residual, *, save=
         xa = [low[:len(part), :len(a)] for a, _ in adapters]
         if save:
             xa[:2] = [buffer[start:start+len(part)] for buffer in saved[2:]]
-        forward_linear(part, matrices[0], *adapters[0], out=gate, xa=xa[0])
-        forward_linear(part, matrices[1], *adapters[1], out=up, xa=xa[1])
+        elif pair is not None:
+            xa[:2] = [pair[:len(part), :r], pair[:len(part), r:]]
+        _gate_up(part, matrices, adapters, gate, up, xa, stack)
         hidden = activation(gate, up, out=workspace[0, :len(part)] if save else gate)
         forward_linear(hidden, matrices[2], *adapters[2], out=destination[start:start+tile], xa=xa[2])
     if residual is not None:
         output.add_(residual)
     return saved
+
+
+def _gate_up(part, matrices, adapters, gate, up, xa, stack):
+    """gate and up of one tile; with `stack` their xa (two column halves of one buffer)
+    come from one GEMM first."""
+    if stack is None or not len(part):
+        forward_linear(part, matrices[0], *adapters[0], out=gate, xa=xa[0])
+        forward_linear(part, matrices[1], *adapters[1], out=up, xa=xa[1])
+        return
+    r = len(adapters[0][0])
+    both = xa[0].as_strided((len(part), 2 * r), xa[0].stride())
+    _low_rank(part, stack, both, transpose=True)
+    matrices[0].forward(part, *adapters[0], None, gate, xa[0], xa_given=True)
+    matrices[1].forward(part, *adapters[1], None, up, xa[1], xa_given=True)
 
 
 class _TiledLoRAMLP(torch.autograd.Function):
@@ -123,13 +147,19 @@ class _TiledLoRAMLP(torch.autograd.Function):
         grad = grad.reshape_as(flat).to(ctx.dtype)
         dx = torch.empty_like(flat) if ctx.needs_input_grad[0] else None
         matrices = _bases(parameters, ctx.states, ctx.dtype)
-        cast = cast_all([parameters[4*i+j] for i in range(3) for j in (1, 2)], ctx.dtype)
+        cast, stack = group_factors(parameters, 3, ctx.dtype, flat, shared=2)
         adapters = [(cast[2*i], cast[2*i+1]) for i in range(3)]
         allocate = torch.empty_like if len(flat) else torch.zeros_like
         gradients = [(allocate(parameters[4*i+1]), allocate(parameters[4*i+2])) for i in range(3)]
         rows = min(ctx.tile, len(flat))
         workspace = torch.empty((3, rows, matrices[0].rows), device=x.device, dtype=ctx.dtype)
-        low_inputs = [torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype) for a, _ in adapters]
+        if stack is not None and not ctx.cache:
+            r = len(adapters[0][0])
+            pair = torch.empty((rows, 2 * r), device=x.device, dtype=ctx.dtype)
+            low_inputs = [pair[:, :r], pair[:, r:],
+                          torch.empty((rows, len(adapters[2][0])), device=x.device, dtype=ctx.dtype)]
+        else:
+            low_inputs = [torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype) for a, _ in adapters]
         low_grad = torch.empty((rows, max(len(a) for a, _ in adapters)), device=x.device, dtype=ctx.dtype)
         for start in range(0, len(flat), ctx.tile):
             part, dy = flat[start:start+ctx.tile], grad[start:start+ctx.tile]
@@ -143,8 +173,7 @@ class _TiledLoRAMLP(torch.autograd.Function):
                 up.copy_(saved[1][start:start+len(part)])
                 xa[:2] = [value[start:start+len(part)] for value in saved[2:]]
             else:
-                forward_linear(part, matrices[0], *adapters[0], out=gate, xa=xa[0])
-                forward_linear(part, matrices[1], *adapters[1], out=up, xa=xa[1])
+                _gate_up(part, matrices, adapters, gate, up, xa, stack)
             input_gradient(dy, matrices[2], *adapters[2], dh, low[2])
             # Reuse the three wide tile buffers: (gate, up, dh) -> (d gate, d up, hidden).
             hidden = activation(gate, up, dh)
