@@ -161,8 +161,11 @@ def test_empty_tiled_inputs_return_zero_parameter_gradients():
 
 @pytest.mark.parametrize("ranks", [(4, 4, 4), (3, 5, 7)])
 @pytest.mark.parametrize("nf4", [False, True])
-def test_shared_qkv_with_bias_and_fp32_adapter_accumulation(ranks, nf4):
-    """tests/test_fast_training.py:95-119 (plus the NF4 base)."""
+@pytest.mark.parametrize("tile", [4, 0])
+def test_shared_qkv_with_bias_and_fp32_adapter_accumulation(ranks, nf4, tile):
+    """tests/test_fast_training.py:95-119 (plus the NF4 base). tile 0 with equal ranks takes
+    the shared xa = x [a_q; a_k; a_v]^T GEMM; tile 4 and unequal ranks the per-projection
+    products."""
     from causal_tuner.kernels.linear import project_group
     from causal_tuner.modeling.lora import Projection
     modules = [Projection(32, out, bias=True, rank=rank, compute_dtype=torch.bfloat16, device="cuda")
@@ -177,7 +180,7 @@ def test_shared_qkv_with_bias_and_fp32_adapter_accumulation(ranks, nf4):
             ref.weight.data.copy_(module.base_weight())
     x = torch.randn(2, 9, 32, device="cuda", dtype=torch.bfloat16, requires_grad=True)
     y = x.detach().clone().requires_grad_(True)
-    outputs = project_group(modules, x, tile=4)
+    outputs = project_group(modules, x, tile=tile)
     targets = [plain_linear(module, y) for module in reference]
     signals = [torch.randn_like(out) for out in outputs]
     torch.autograd.backward(outputs, signals)
@@ -304,3 +307,29 @@ def test_merged_weight_is_the_effective_linear_map(nf4):
     via_forward = module(x).float()
     assert ((via_merged - via_forward).norm() / via_forward.norm()).item() <= 1e-2
     assert module.merged_weight(torch.float32).dtype == torch.float32
+
+
+def test_shared_group_with_bf16_adapters():
+    """bf16 LoRA factors (no cast): the stacked factors are copies; outputs and gradients
+    against the independent autograd formulation."""
+    from causal_tuner.kernels.linear import project_group
+    from causal_tuner.modeling.lora import Projection
+    torch.manual_seed(2)
+    modules = [Projection(64, out, bias=True, rank=8, train_dtype=torch.bfloat16, device="cuda")
+               for out in (64, 16, 16)]
+    for module in modules:
+        torch.nn.init.normal_(module.lora_B, std=.1)
+        module.install_nf4(module.weight.detach().clone(), "cuda")
+    x = torch.randn(3, 11, 64, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    y = x.detach().clone().requires_grad_(True)
+    outputs = project_group(modules, x)
+    targets = [plain_linear(module, y) for module in modules]
+    signals = [torch.randn_like(out) for out in outputs]
+    params = [p for m in modules for p in (m.lora_A, m.lora_B)]
+    got = torch.autograd.grad(outputs, [x, *params], signals)
+    want = torch.autograd.grad(targets, [y, *params], signals)
+    for out, target in zip(outputs, targets):
+        torch.testing.assert_close(out, target, rtol=.03, atol=.02)
+    for a, b in zip(got, want):
+        assert a.dtype == b.dtype
+        assert ((a.float() - b.float()).norm() / b.float().norm()).item() < .03
