@@ -58,7 +58,10 @@ class FusedAdamW(torch.optim.Optimizer):
         table = torch.tensor([list(r) for r in rows], dtype=torch.int64).reshape(-1, 6)
         chunks = [(index, start) for index, r in enumerate(rows) for start in range(0, r[5], _CHUNK)]
         chunk_list = torch.tensor(chunks, dtype=torch.int64).reshape(-1, 2)
-        entry = (key, table.to(device, non_blocking=False), chunk_list.to(device, non_blocking=False))
+        # Pinned host copies go up asynchronously on the current stream (no host wait); the
+        # pinned allocator keeps their blocks until the copies are done.
+        entry = (key, table.pin_memory().to(device, non_blocking=True),
+                 chunk_list.pin_memory().to(device, non_blocking=True))
         self._tables[slot] = entry
         return entry[1], entry[2]
 

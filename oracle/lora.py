@@ -98,7 +98,7 @@ def projection_flops(m, k, n, r):
 
 def relative_error(actual, expected):
     """(max|a-r| / max|r|, ||a-r|| / ||r||) in float64."""
-    a, r = actual.double(), expected.double()
+    a, r = actual.detach().double(), expected.detach().double()
     diff = (a - r).abs()
     scale = r.abs().max().clamp_min(1e-300)
     return float(diff.max() / scale), float((a - r).norm() / r.norm().clamp_min(1e-300))
