@@ -59,7 +59,8 @@ _SIGNATURES = {
     "ct_rms_forward": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _P, _I64, _I64, ctypes.c_float, _P]),
     "ct_rms_backward_workspace": (_I64, [_I64, _I64, _I32]),
     "ct_rms_backward": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _P, _P, _P, _I64, _I64, _I32, _P, _I64, _P]),
-    "ct_weighted_ce": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _P, _P, _P, _I32, _P]),
+    "ct_weighted_ce_workspace": (_I64, [_I64, _I64]),
+    "ct_weighted_ce": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _P, _P, _P, _I32, _P, _I64, _P]),
     "ct_cast_f32_bf16": (ctypes.c_int, [_P, _P, _P, _I32, _P]),
     "ct_adamw_step": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _I32, ctypes.c_double, ctypes.c_double,
                                      ctypes.c_double, ctypes.c_double, ctypes.c_double, _I32, _I32, _P]),

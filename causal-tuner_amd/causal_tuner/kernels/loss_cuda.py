@@ -3,14 +3,16 @@ kernels/loss_cuda.py).
 
 `weighted_ce` (loss_cuda.py:11-70) keeps the reference's signature and contract: per-row
 weighted losses, and with `gradient=True` the logits overwritten in place by the weighted
-softmax derivative. It runs the HIP kernel ct_weighted_ce (one workgroup per row, fixed
-reduction order); the `partials` workspace of the reference's split statistics is accepted
-and not needed. `FusedProjectionLoss` (loss_cuda.py:81-162) drives it tile by tile.
+softmax derivative. It runs the HIP kernel ct_weighted_ce (4096-column splits per row as
+the reference's _statistics/_finish, fixed reduction order) with its own workspace; the
+reference's `partials` argument is accepted and not needed. `FusedProjectionLoss` (loss_cuda.py:81-162) drives it tile by tile.
 """
 
 import torch
 
 from . import _native
+
+_CE_ROWS = 65535  # rows per ct_weighted_ce call
 
 
 def weighted_ce(logits, targets, weights, *, gradient, loss=None, partials=None):
@@ -24,11 +26,16 @@ def weighted_ce(logits, targets, weights, *, gradient, loss=None, partials=None)
         loss = torch.empty(rows, device=logits.device, dtype=torch.float32)
     targets = targets.to(torch.int64).contiguous()
     weights = weights.to(torch.float32).contiguous()
-    if rows:
+    lib = _native.library()
+    for start in range(0, rows, _CE_ROWS):
+        part = min(_CE_ROWS, rows - start)
+        workspace = torch.empty(max(lib.ct_weighted_ce_workspace(part, vocab), 1), dtype=torch.uint8,
+                                device=logits.device)
         with torch.cuda.device(logits.device):
-            status = _native.library().ct_weighted_ce(
-                _native.ptr(logits), _native.dtype_code(logits.dtype), rows, vocab, logits.stride(0),
-                _native.ptr(targets), _native.ptr(weights), _native.ptr(loss), int(bool(gradient)),
+            status = lib.ct_weighted_ce(
+                _native.ptr(logits[start:start + part]), _native.dtype_code(logits.dtype), part, vocab,
+                logits.stride(0), _native.ptr(targets[start:start + part]), _native.ptr(weights[start:start + part]),
+                _native.ptr(loss[start:start + part]), int(bool(gradient)), _native.ptr(workspace), workspace.numel(),
                 _native.stream_of(logits))
         _native.check(status, "ct_weighted_ce")
     return loss

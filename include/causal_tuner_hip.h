@@ -174,11 +174,14 @@ int ct_rms_backward(const void *x, int32_t x_dtype, const void *w, int32_t w_dty
  *   lse[r] = log sum_c exp(logits[r, c]);  loss[r] = weights[r] * (lse[r] - logits[r, target[r]])
  * (the target term is 0 for a target outside [0, vocab)). With gradient != 0 the logits
  * are overwritten with (exp(logits - lse) - onehot(target)) * weights[r], rounded to dtype.
- * Deterministic (fixed reduction order).
+ * Two launches over 4096-column splits of each row; the workspace (8-byte aligned,
+ * ct_weighted_ce_workspace bytes) holds the per-split (maximum, sum) pairs and the target
+ * logits. At most 65535 rows per call. Deterministic (fixed reduction order).
  */
+int64_t ct_weighted_ce_workspace(int64_t rows, int64_t vocab);
 int ct_weighted_ce(void *logits, int32_t dtype, int64_t rows, int64_t vocab, int64_t ld,
                    const int64_t *targets, const float *weights, float *loss, int32_t gradient,
-                   hipStream_t stream);
+                   void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * Replaces the optimizer step of torch.optim.AdamW(fused=True) as the reference builds it

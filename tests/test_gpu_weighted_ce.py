@@ -63,3 +63,34 @@ def test_weighted_ce_against_float64_and_repeatable():
     want = torch.zeros_like(sums)
     want[3] = weights[3]
     torch.testing.assert_close(sums, want, rtol=0, atol=3e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("pad", [0, 3])
+def test_weighted_ce_row_pitch_and_split_edges(dtype, pad):
+    """Rows with a pitch past the vocabulary (pad 3: rows not 16-byte aligned, so the
+    per-element path) and a vocabulary just past two 4096-column splits, against float64;
+    the columns past the vocabulary are never written."""
+    from causal_tuner.kernels.loss_cuda import weighted_ce
+    rows, vocab = 9, 8192 + 5
+    g = torch.Generator(device="cuda").manual_seed(8)
+    storage = (torch.randn(rows, vocab + pad, device="cuda", generator=g) * 2).to(dtype)
+    logits = storage[:, :vocab]
+    targets = torch.tensor([0, 4095, 4096, 8191, 8192, vocab - 1, 17, -1, vocab], device="cuda")
+    weights = torch.rand(rows, device="cuda", generator=g) + 0.5
+    l64 = logits.double()
+    lse = torch.logsumexp(l64, dim=1)
+    inside = (targets >= 0) & (targets < vocab)
+    picked = torch.where(inside, l64.gather(1, targets.clamp(0, vocab - 1)[:, None])[:, 0], torch.zeros_like(lse))
+    want_loss = weights.double() * (lse - picked)
+    soft = torch.softmax(l64, dim=1)
+    onehot = torch.zeros_like(soft)
+    onehot[inside.nonzero()[:, 0], targets[inside]] = 1
+    want_grad = (soft - onehot) * weights.double()[:, None]
+    before = storage.clone()
+    loss = weighted_ce(logits, targets, weights, gradient=True)
+    torch.testing.assert_close(loss.double(), want_loss, rtol=1e-5, atol=1e-5)
+    tol = {torch.float32: 1e-6, torch.bfloat16: 8e-3, torch.float16: 1e-3}[dtype]
+    torch.testing.assert_close(logits.double(), want_grad.to(dtype).double(), rtol=tol, atol=1e-6)
+    if pad:
+        assert torch.equal(storage[:, vocab:], before[:, vocab:])
