@@ -8,12 +8,15 @@
 //             from output: n = y / T(w),  gx = inverse * (g - n * (sum(g * n) / width))
 //             dw = sum over rows of go * T(x * inverse)            (fp32, rounded to w's dtype)
 //
-// One wave per row for the row passes (wave-level shuffle reduction, fixed order); the
+// One wave per row for the row passes (wave-level shuffle reduction, fixed order; 16-byte
+// loads with the row kept in registers for 16-bit tensors up to 4096 wide); the
 // weight gradient is summed over fixed row groups (one lane per column and group, rows in
 // order) and then over the groups in order, so every result is reproducible bit for bit.
 // The row sums' order differs from the reference's Triton reduction, and the reciprocal
 // square root is an IEEE division of an IEEE square root: results agree with the
 // reference to the rounding of the stored dtype, not bit for bit.
+
+#include <initializer_list>
 
 #include "common.hpp"
 
@@ -96,6 +99,140 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void rms_input_grad(const void 
     }
 }
 
+// ---------------------------------------------------------------- 16-byte row passes
+// 16-bit activations and weights, width a multiple of 8 up to 64 * 8 * kVecChunks: lane l
+// of the row's wave holds elements 512 j + 8 l .. + 7 of chunk j, loaded once as 16 bytes
+// and kept in registers for the second pass (the row is read from HBM once).
+constexpr int kVecChunks = 8;
+
+template <int DT>
+__device__ __forceinline__ float half_to_f32(uint32_t word, int hi) {
+    const uint16_t h = (uint16_t)(hi ? word >> 16 : word & 0xffffu);
+    return DT == CT_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+template <int DT>
+__device__ __forceinline__ float vec_elem(const uint4 &q, int e) {
+    const uint32_t w = e < 2 ? q.x : e < 4 ? q.y : e < 6 ? q.z : q.w;
+    return half_to_f32<DT>(w, e & 1);
+}
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    if constexpr (DT == CT_BF16) return pack_bf16x2(lo, hi);
+    else return (uint32_t)f16_bits(lo) | ((uint32_t)f16_bits(hi) << 16);
+}
+
+template <int XT, int WT>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void rms_forward_vec(const void *__restrict__ x,
+                                                                     const void *__restrict__ w,
+                                                                     void *__restrict__ y, float *__restrict__ rstd,
+                                                                     int64_t rows, int64_t width, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;  // wave-uniform
+    const uint4 *xr = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + row * width);
+    const int n = (int)(width / 8);  // 16-byte groups in the row
+    uint4 v[kVecChunks];
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kVecChunks; ++j) {
+        const int g = j * 64 + lane;
+        v[j] = g < n ? xr[g] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < kVecChunks; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float t = vec_elem<XT>(v[j], e);
+            s += t * t;
+        }
+    s = wave_sum(s);
+    const float inverse = 1.0f / sqrtf(s / (float)width + eps);
+    const uint4 *wr = reinterpret_cast<const uint4 *>(w);
+    uint4 *yr = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(y) + row * width);
+#pragma unroll
+    for (int j = 0; j < kVecChunks; ++j) {
+        const int g = j * 64 + lane;
+        if (g >= n) continue;
+        const uint4 wq = wr[g];
+        uint32_t out[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            float o[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float normalized = round_to_storage<XT>(vec_elem<XT>(v[j], e + h) * inverse);
+                const float weight = round_to_storage<XT>(vec_elem<WT>(wq, e + h));
+                o[h] = normalized * weight;
+            }
+            out[e / 2] = pack2<XT>(o[0], o[1]);
+        }
+        yr[g] = make_uint4(out[0], out[1], out[2], out[3]);
+    }
+    if (lane == 0) rstd[row] = inverse;
+}
+
+// Input gradient on 16-byte groups; gx may alias go (each lane rewrites only the groups it
+// read).
+template <int XT, int WT, bool FROM_OUTPUT>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void rms_input_grad_vec(const void *__restrict__ x,
+                                                                        const void *__restrict__ w,
+                                                                        const float *__restrict__ rstd,
+                                                                        const void *go, void *gx, int64_t rows,
+                                                                        int64_t width) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int n = (int)(width / 8);
+    const uint4 *xr = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + row * width);
+    const uint4 *gr = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(go) + row * width);
+    const uint4 *wr = reinterpret_cast<const uint4 *>(w);
+    const float inverse = rstd[row];
+    uint4 xv[kVecChunks], gv[kVecChunks], wv[kVecChunks];
+#pragma unroll
+    for (int j = 0; j < kVecChunks; ++j) {
+        const int g = j * 64 + lane;
+        const bool ok = g < n;
+        xv[j] = ok ? xr[g] : make_uint4(0, 0, 0, 0);
+        gv[j] = ok ? gr[g] : make_uint4(0, 0, 0, 0);
+        wv[j] = ok ? wr[g] : make_uint4(0, 0, 0, 0);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kVecChunks; ++j) {
+        if (j * 64 + lane >= n) continue;  // past the row (zero weights would divide 0 by 0)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float weight = round_to_storage<XT>(vec_elem<WT>(wv[j], e));
+            const float g = round_to_storage<XT>(vec_elem<XT>(gv[j], e) * weight);
+            const float v = vec_elem<XT>(xv[j], e);
+            s += g * (FROM_OUTPUT ? v / weight : v);
+        }
+    }
+    const float projection = wave_sum(s) / (float)width;
+    const float factor = FROM_OUTPUT ? projection : inverse * inverse * projection;
+    uint4 *dr = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(gx) + row * width);
+#pragma unroll
+    for (int j = 0; j < kVecChunks; ++j) {
+        const int g = j * 64 + lane;
+        if (g >= n) continue;
+        uint32_t out[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            float o[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float weight = round_to_storage<XT>(vec_elem<WT>(wv[j], e + h));
+                const float gg = round_to_storage<XT>(vec_elem<XT>(gv[j], e + h) * weight);
+                const float v = vec_elem<XT>(xv[j], e + h);
+                const float operand = FROM_OUTPUT ? v / weight : v;
+                o[h] = inverse * (gg - operand * factor);
+            }
+            out[e / 2] = pack2<XT>(o[0], o[1]);
+        }
+        dr[g] = make_uint4(out[0], out[1], out[2], out[3]);
+    }
+}
+
 // Weight-gradient partials: partial[group][c] = sum over the group's rows, in order, of
 // go * T(x * inverse).
 template <int XT>
@@ -143,11 +280,31 @@ void weight_groups(int64_t rows, int64_t *groups, int64_t *rows_per_group) {
 
 bool valid(int d) { return d == CT_F32 || d == CT_F16 || d == CT_BF16; }
 
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// The 16-byte row kernels: 16-bit activations and weights, width a multiple of 8 and at
+// most 64 * 8 * kVecChunks, every row pointer 16-byte aligned.
+template <int XT, int WT>
+constexpr bool kVecTypes = (XT == CT_BF16 || XT == CT_F16) && (WT == CT_BF16 || WT == CT_F16);
+
+bool vec_rows(int64_t width, std::initializer_list<const void *> ptrs) {
+    if (width % 8 || width > 64 * 8 * kVecChunks) return false;
+    for (const void *p : ptrs)
+        if (p && !aligned16(p)) return false;
+    return true;
+}
+
 template <int XT, int WT>
 hipError_t forward_typed(const void *x, const void *w, void *y, float *rstd, int64_t rows, int64_t width, float eps,
                          hipStream_t s) {
-    rms_forward<XT, WT><<<dim3((unsigned)cdiv(rows, kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0, s>>>(
-        x, w, y, rstd, rows, width, eps);
+    const dim3 grid((unsigned)cdiv(rows, kRowsPerBlock)), block(64 * kRowsPerBlock);
+    if constexpr (kVecTypes<XT, WT>) {
+        if (vec_rows(width, {x, w, y})) {
+            rms_forward_vec<XT, WT><<<grid, block, 0, s>>>(x, w, y, rstd, rows, width, eps);
+            return hipGetLastError();
+        }
+    }
+    rms_forward<XT, WT><<<grid, block, 0, s>>>(x, w, y, rstd, rows, width, eps);
     return hipGetLastError();
 }
 
@@ -157,8 +314,16 @@ hipError_t backward_typed(const void *x, const void *w, const float *rstd, const
                           int64_t rows_per_group, hipStream_t s) {
     if (gx) {
         const dim3 grid((unsigned)cdiv(rows, kRowsPerBlock)), block(64 * kRowsPerBlock);
-        if (from_output) rms_input_grad<XT, WT, true><<<grid, block, 0, s>>>(x, w, rstd, go, gx, rows, width);
-        else rms_input_grad<XT, WT, false><<<grid, block, 0, s>>>(x, w, rstd, go, gx, rows, width);
+        bool done = false;
+        if constexpr (kVecTypes<XT, WT>) {
+            if (vec_rows(width, {x, w, go, gx})) {
+                if (from_output) rms_input_grad_vec<XT, WT, true><<<grid, block, 0, s>>>(x, w, rstd, go, gx, rows, width);
+                else rms_input_grad_vec<XT, WT, false><<<grid, block, 0, s>>>(x, w, rstd, go, gx, rows, width);
+                done = true;
+            }
+        }
+        if (!done && from_output) rms_input_grad<XT, WT, true><<<grid, block, 0, s>>>(x, w, rstd, go, gx, rows, width);
+        else if (!done) rms_input_grad<XT, WT, false><<<grid, block, 0, s>>>(x, w, rstd, go, gx, rows, width);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
