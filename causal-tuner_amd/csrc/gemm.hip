@@ -1359,13 +1359,18 @@ extern "C" int ct_nf4_fused_supported(const ct_nf4_weight *w) { return nf4_fusab
 
 namespace ct {
 namespace {
-// Rank-r products (at most 256 columns, many rows, a long reduction): 128-wide tiles with
-// the reduction split 4 ways fill the GPU better than 64-wide tiles (measured on MI355X
-// at 8192 rows: 20-25% faster for reductions of 11008).
+// Rank-r products (narrow outputs: r columns, or up to 1024 for a group's stacked factors;
+// many rows; a long reduction): when 128 x 128 tiles give less than one workgroup per CU,
+// the reduction is split 2 to 4 ways (about 512 workgroups, two per CU). Measured on
+// MI355X: at 8192 rows and 256 columns 20-25% faster than 64-wide tiles for reductions of
+// 11008; at 4096 rows the stacked q/k/v and gate/up products likewise.
 bool lowrank_split(int64_t m, int64_t n, int64_t k, int *tile, int *splits) {
-    if (n > 256 || m < 4096 || k < 2048) return false;
+    if (n > 1024 || m < 4096 || k < 2048) return false;
+    const int64_t tiles = cdiv(m, 128) * cdiv(n, 128);
+    if (tiles >= 256) return false;
+    int64_t s = 512 / tiles;
     *tile = TILE_128;
-    *splits = 4;
+    *splits = (int)(s < 2 ? 2 : (s > 4 ? 4 : s));
 #ifdef CT_TUNING
     if (const char *env = getenv("CT_LOWRANK")) {
         int t = 0, sp = 0;
