@@ -6,6 +6,7 @@ boundary therefore belong to the same runtime. A missing library raises RuntimeE
 there is no fallback.
 """
 
+import contextlib
 import ctypes
 import os
 
@@ -103,13 +104,29 @@ def check(status, what):
         raise RuntimeError(f"{what} failed with status {status}: {message}")
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_CURRENT = contextlib.nullcontext()
+
+
 def stream_of(tensor):
-    """The caller's current HIP stream on the tensor's device (kernels never pick their own)."""
-    return ctypes.c_void_p(torch.cuda.current_stream(tensor.device).cuda_stream)
+    """The caller's current HIP stream on the tensor's device (kernels never pick their own),
+    as the integer handle the `void *` arguments take."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(tensor.device.index)
+    return torch.cuda.current_stream(tensor.device).cuda_stream
+
+
+def device_of(tensor):
+    """A context making the tensor's device current for a launch: a no-op when it already is
+    (the usual single-device case costs one device query instead of two device switches)."""
+    index = tensor.device.index
+    if index == torch.cuda.current_device():
+        return _CURRENT
+    return torch.cuda.device(index)
 
 
 def ptr(tensor):
-    return None if tensor is None else ctypes.c_void_p(tensor.data_ptr())
+    return None if tensor is None else tensor.data_ptr()
 
 
 def dtype_code(dtype):

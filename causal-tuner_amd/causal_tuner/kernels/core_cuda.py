@@ -34,7 +34,7 @@ class RMS(torch.autograd.Function):
         output = torch.empty_like(x)
         width = x.shape[-1]
         inverse = torch.empty(x.numel() // width if width else 0, device=x.device, dtype=torch.float32)
-        with torch.cuda.device(x.device):
+        with _native.device_of(x):
             status = _native.library().ct_rms_forward(
                 _native.ptr(x), _native.dtype_code(x.dtype), _native.ptr(weight.contiguous()),
                 _native.dtype_code(weight.dtype), _native.ptr(output), _native.ptr(inverse), len(inverse), width,
@@ -56,7 +56,7 @@ class RMS(torch.autograd.Function):
         ws_bytes = lib.ct_rms_backward_workspace(rows, width, int(dw is not None))
         workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
         if result is not None or dw is not None:
-            with torch.cuda.device(x.device):
+            with _native.device_of(x):
                 status = lib.ct_rms_backward(
                     _native.ptr(x), _native.dtype_code(x.dtype), _native.ptr(weight.contiguous()),
                     _native.dtype_code(weight.dtype), _native.ptr(inverse), _native.ptr(grad), _native.ptr(result),
@@ -86,7 +86,7 @@ def _rope(x, y, cosine, sine, head_dim, *, inverse, rotated_only):
         tokens, heads = 1, x.numel() // head_dim
     if x.numel() == 0:
         return y
-    with torch.cuda.device(x.device):
+    with _native.device_of(x):
         status = _native.library().ct_rope(
             _native.ptr(x), _native.ptr(y), _native.ptr(cosine), _native.ptr(sine), tokens, heads, head_dim, half,
             int(inverse), int(rotated_only), _native.dtype_code(x.dtype), _native.dtype_code(cosine.dtype),

@@ -102,32 +102,29 @@ def cast_all(tensors, dtype, outputs=None):
     (kernels/linear.py:70,108; kernels/mlp_cuda.py:62,110)."""
     outputs = outputs or [None] * len(tensors)
     out = [None] * len(tensors)
-    batch = [i for i, t in enumerate(tensors)
-             if dtype == torch.bfloat16 and t.dtype == torch.float32 and t.is_cuda and t.is_contiguous()
-             and t.numel()]
+    batch = ([i for i, t in enumerate(tensors) if t.dtype == torch.float32 and t.is_cuda and t.is_contiguous()
+              and t.numel()] if dtype == torch.bfloat16 else [])
     if len(batch) > 1 or any(outputs[i] is not None for i in batch):
-        lib = _native.library()
-        fresh = [i for i in batch if outputs[i] is None]
-        padded = [(tensors[i].numel() + 7) // 8 * 8 for i in fresh]   # 16-byte aligned views
-        buffer = torch.empty(sum(padded), dtype=torch.bfloat16, device=tensors[batch[0]].device)
-        offset = 0
-        for i, size in zip(fresh, padded):
-            out[i] = buffer[offset:offset + tensors[i].numel()].view(tensors[i].shape)
-            offset += size
+        first = tensors[batch[0]]
+        fresh = []
         for i in batch:
-            if outputs[i] is not None:
-                out[i] = outputs[i]
-        limit = _native.CT_CAST_MAX
-        for first in range(0, len(batch), limit):
-            part = batch[first:first + limit]
-            src = (ctypes.c_void_p * len(part))(*[tensors[i].data_ptr() for i in part])
-            dst = (ctypes.c_void_p * len(part))(*[out[i].data_ptr() for i in part])
-            counts = (ctypes.c_int64 * len(part))(*[tensors[i].numel() for i in part])
-            with torch.cuda.device(tensors[batch[0]].device):
-                status = lib.ct_cast_f32_bf16(ctypes.cast(src, ctypes.c_void_p), ctypes.cast(dst, ctypes.c_void_p),
-                                              ctypes.cast(counts, ctypes.c_void_p), len(part),
-                                              _native.stream_of(tensors[batch[0]]))
-            _native.check(status, "ct_cast_f32_bf16")
+            out[i] = outputs[i]
+            if out[i] is None:
+                fresh.append(i)
+        sizes = [tensors[i].numel() for i in fresh]
+        buffer = torch.empty(sum((n + 7) // 8 * 8 for n in sizes), dtype=torch.bfloat16, device=first.device)
+        offset = 0
+        for i, n in zip(fresh, sizes):
+            out[i] = buffer[offset:offset + n].view(tensors[i].shape)
+            offset += (n + 7) // 8 * 8   # 16-byte aligned views
+        lib, stream, limit = _native.library(), _native.stream_of(first), _native.CT_CAST_MAX
+        with _native.device_of(first):
+            for start in range(0, len(batch), limit):
+                part = batch[start:start + limit]
+                src = (ctypes.c_void_p * len(part))(*[tensors[i].data_ptr() for i in part])
+                dst = (ctypes.c_void_p * len(part))(*[out[i].data_ptr() for i in part])
+                counts = (ctypes.c_int64 * len(part))(*[tensors[i].numel() for i in part])
+                _native.check(lib.ct_cast_f32_bf16(src, dst, counts, len(part), stream), "ct_cast_f32_bf16")
     result = [t.to(dtype) if o is None else o for t, o in zip(tensors, out)]
     for i, o in enumerate(outputs):
         if o is not None and result[i] is not o:
@@ -183,7 +180,7 @@ def accumulate(output, left, right, *, add=True):
         rt, ldr, tr = _operand(right)
         lib = _native.library()
         ws = _workspace(lib.ct_accumulate_workspace(p, q, j), output.device)
-        with torch.cuda.device(output.device):
+        with _native.device_of(output):
             status = lib.ct_accumulate(_native.ptr(target.buffer), target.ld, _native.ptr(lt), ldl, tl,
                                        _native.ptr(rt), ldr, tr, p, q, j, int(add) if target.buffer is output else
                                        0, _native.ptr(ws), ws.numel(), _native.stream_of(output))
@@ -228,7 +225,7 @@ def _forward(x, weight, state, a, b, bias, out, xa, xa_given=False):
     desc = None if state is None else _native.nf4_descriptor(w, state)
     lib = _native.library()
     ws = _workspace(lib.ct_forward_linear_workspace(m, n, k, r, _native.nf4_kind(desc)), x.device)
-    with torch.cuda.device(x.device):
+    with _native.device_of(x):
         status = lib.ct_forward_linear(
             _native.ptr(x), ldx, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),
             _native.ptr(b), _native.ptr(bias), _native.ptr(target.buffer), target.ld, _native.ptr(low.buffer),
@@ -265,7 +262,7 @@ def _input_gradient(dy, weight, state, a, b, dx, low, add):
     desc = None if state is None else _native.nf4_descriptor(w, state)
     lib = _native.library()
     ws = _workspace(lib.ct_input_gradient_workspace(m, n, k, r, _native.nf4_kind(desc)), dy.device)
-    with torch.cuda.device(dy.device):
+    with _native.device_of(dy):
         status = lib.ct_input_gradient(
             _native.ptr(dy), lddy, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),
             _native.ptr(b), _native.ptr(target.buffer), target.ld, _native.ptr(lowc.buffer), m, n, k, r, int(add),
@@ -296,7 +293,7 @@ def parameter_gradients(x, dy, da, db, low, xa, *, add):
         return
     lib = _native.library()
     ws = _workspace(lib.ct_parameter_gradients_workspace(m, n, k, r), x.device)
-    with torch.cuda.device(x.device):
+    with _native.device_of(x):
         status = lib.ct_parameter_gradients(_native.ptr(x), ldx, _native.ptr(dy), lddy, _native.ptr(low), ldlow,
                                              _native.ptr(xa), ldxa, _native.ptr(da), _native.ptr(db), m, n, k, r,
                                              int(add), _native.ptr(ws), ws.numel(), _native.stream_of(x))
@@ -457,7 +454,7 @@ def _low_rank(x, factor, out, *, transpose):
     target = _Output(out)
     lib = _native.library()
     ws = _workspace(lib.ct_gemm_workspace(m, r, k, 0, int(transpose), _native.CT_BF16), x.device)
-    with torch.cuda.device(x.device):
+    with _native.device_of(x):
         status = lib.ct_gemm(_native.ptr(x), ldx, 0, _native.ptr(factor), k if transpose else r, int(transpose),
                              _native.ptr(target.buffer), target.ld, _native.CT_BF16, None, 0, m, r, k,
                              _native.ptr(ws), ws.numel(), _native.stream_of(x))

@@ -31,7 +31,7 @@ def weighted_ce(logits, targets, weights, *, gradient, loss=None, partials=None)
         part = min(_CE_ROWS, rows - start)
         workspace = torch.empty(max(lib.ct_weighted_ce_workspace(part, vocab), 1), dtype=torch.uint8,
                                 device=logits.device)
-        with torch.cuda.device(logits.device):
+        with _native.device_of(logits):
             status = lib.ct_weighted_ce(
                 _native.ptr(logits[start:start + part]), _native.dtype_code(logits.dtype), part, vocab,
                 logits.stride(0), _native.ptr(targets[start:start + part]), _native.ptr(weights[start:start + part]),

@@ -20,7 +20,7 @@ def _silu(gate, up, h, dg, du, backward, reconstruct):
     code = _native.dtype_code(gate.dtype)
     if code == _native.CT_F16:
         raise NotImplementedError("activation: the HIP kernel takes bfloat16 or float32")
-    with torch.cuda.device(gate.device):
+    with _native.device_of(gate):
         status = _native.library().ct_silu_multiply(
             _native.ptr(gate), _native.ptr(up), _native.ptr(h), _native.ptr(dg), _native.ptr(du), gate.numel(),
             int(backward), int(reconstruct), code, _native.stream_of(gate))

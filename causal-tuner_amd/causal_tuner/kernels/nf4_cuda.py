@@ -28,7 +28,7 @@ def dequantize_nf4_into(weight, state, output):
     if not output.is_contiguous() or output.numel() != state.shape.numel():
         raise ValueError("NF4 output must be contiguous with the state's element count")
     desc = _native.nf4_descriptor(weight, state)
-    with torch.cuda.device(weight.device):
+    with _native.device_of(weight):
         status = _native.library().ct_nf4_dequant(desc, _native.ptr(output), _native.dtype_code(output.dtype),
                                                   _native.stream_of(output))
     _native.check(status, "ct_nf4_dequant")
