@@ -60,13 +60,18 @@ def _attention(q, k, v, records):
     """Causal attention inside each record. q [1, S, H, D]; k, v [1, S, 1, D]."""
     from torch.nn.attention import SDPBackend, sdpa_kernel
     heads = q.shape[2]
+    sizes = [stop - start for start, stop in records]
+    if sum(sizes) != q.shape[1]:
+        raise ValueError("records must cover the sequence")
     outputs = []
+    # One split per tensor: its backward concatenates the records' gradients in one
+    # launch (a slice per record would fill and add a full-size gradient each).
     # Only the fused backends: never the math fallback.
     with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-        for start, stop in records:
-            qs = q[:, start:stop].transpose(1, 2)
-            ks = k[:, start:stop].transpose(1, 2).expand(-1, heads, -1, -1)
-            vs = v[:, start:stop].transpose(1, 2).expand(-1, heads, -1, -1)
+        for qs, ks, vs in zip(q.split(sizes, dim=1), k.split(sizes, dim=1), v.split(sizes, dim=1)):
+            qs = qs.transpose(1, 2)
+            ks = ks.transpose(1, 2).expand(-1, heads, -1, -1)
+            vs = vs.transpose(1, 2).expand(-1, heads, -1, -1)
             outputs.append(F.scaled_dot_product_attention(qs, ks, vs, is_causal=True).transpose(1, 2))
     return torch.cat(outputs, dim=1)
 
