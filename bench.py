@@ -430,7 +430,7 @@ def c4_measure(device, steps=5, warmup=2):
               "records": [b - a for a, b in records], "tokens_per_s": round(seq / (ms * 1e-3), 1),
               "ms_per_step": round(ms, 3), "steps": steps, "warmup": warmup,
               "trainable_params": sum(p.numel() for p in params), "loss": round(float(loss.detach()), 4),
-              "attention": "torch SDPA (flash backend), causal per record",
+              "attention": "torch SDPA (memory-efficient backend), causal per record",
               "peak_mem_GiB": round(torch.cuda.max_memory_allocated() / 2**30, 2)}
     del model, opt, params
     torch.cuda.empty_cache()
