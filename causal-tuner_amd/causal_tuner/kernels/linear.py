@@ -349,14 +349,17 @@ class _Base:
 
 
 class _LoRAGroup(torch.autograd.Function):
-    """Projections sharing one input; saves only the input and parameters (linear.py:59-130).
+    """Projections sharing one input (linear.py:59-130). Saves the input and parameters and,
+    when one tile covers all rows, each projection's forward xa = x a^T ([rows, r], 4 MB at
+    8192 x 256 in bf16), which the reference recomputes in the backward (linear.py:124-125):
+    the backward then reads the same values instead of running the rank-r GEMMs again.
 
     Without an explicit tile the backward runs each projection over all rows at once (the
-    rank-r workspaces are [rows, r]); an explicit tile bounds them as in the reference."""
+    rank-r workspaces are [rows, r]); an explicit tile bounds them as in the reference and
+    keeps its recompute."""
 
     @staticmethod
     def forward(ctx, x, dtype, tile, states, cosine, sine, head_dim, residual, *parameters):
-        ctx.save_for_backward(x, cosine, sine, *parameters)
         ctx.dtype, ctx.tile, ctx.states = dtype, tile, states
         ctx.head_dim = head_dim
         flat = x.reshape(-1, x.shape[-1]).to(dtype)
@@ -368,6 +371,7 @@ class _LoRAGroup(torch.autograd.Function):
         # factors (the same products; the fp32 sums may be split differently than in
         # separate launches, so a value can differ by one bf16 rounding).
         shared = _shared_xa(flat, stack) if stack is not None and 0 < len(flat) <= step else None
+        kept = []   # each projection's xa over all rows, for the backward
         for index, state in enumerate(states):
             weight, a, b, bias = parameters[index*4:index*4+4]
             base, ac, bc = _Base(weight, state, dtype), factors[2*index], factors[2*index+1]
@@ -375,16 +379,22 @@ class _LoRAGroup(torch.autograd.Function):
             out = torch.empty((len(flat), base.rows), device=x.device, dtype=dtype)
             if shared is not None:
                 r = len(a)
-                base.forward(flat, ac, bc, bias, out, shared[:, index*r:(index+1)*r], xa_given=True)
+                kept.append(shared[:, index*r:(index+1)*r])
+                base.forward(flat, ac, bc, bias, out, kept[-1], xa_given=True)
             else:
                 low = torch.empty((rows, len(a)), device=x.device, dtype=dtype)
                 for start in range(0, len(flat), step):
                     part = flat[start:start+step]
                     base.forward(part, ac, bc, bias, out[start:start+step], low[:len(part)])
+                kept.append(low)
                 del low
             outputs.append(out.reshape(*x.shape[:-1], base.rows))
             del base, ac, bc
-        del factors, stack, shared
+        if not 0 < len(flat) <= step:
+            kept = []   # tiled (xa of the last tile only) or empty: the backward recomputes
+        ctx.kept = len(kept)
+        ctx.save_for_backward(x, cosine, sine, *parameters, *kept)
+        del factors, stack, shared, kept
         if head_dim:
             from .core_cuda import rotate_owned_qk
             rotate_owned_qk(outputs[0], outputs[1], cosine, sine, head_dim)
@@ -395,6 +405,8 @@ class _LoRAGroup(torch.autograd.Function):
     @staticmethod
     def backward(ctx, *grad_outputs):
         x, cosine, sine, *parameters = ctx.saved_tensors
+        kept = parameters[len(parameters)-ctx.kept:] if ctx.kept else None
+        parameters = parameters[:len(parameters)-ctx.kept]
         flat = x.reshape(-1, x.shape[-1]).to(ctx.dtype)
         dx = torch.empty_like(flat) if ctx.needs_input_grad[0] else None
         if ctx.head_dim:
@@ -405,7 +417,8 @@ class _LoRAGroup(torch.autograd.Function):
                   if ctx.head_dim else None)
         results = []
         factors, stack = group_factors(parameters, len(ctx.states), ctx.dtype, x)
-        shared = _shared_xa(flat, stack) if stack is not None and 0 < len(flat) <= step else None
+        shared = (_shared_xa(flat, stack) if kept is None and stack is not None and 0 < len(flat) <= step
+                  else None)
         for index, (state, grad) in enumerate(zip(ctx.states, grad_outputs)):
             weight, a, b, _ = parameters[index*4:index*4+4]
             base = _Base(weight, state, ctx.dtype) if dx is not None else None
@@ -414,7 +427,7 @@ class _LoRAGroup(torch.autograd.Function):
             allocate = torch.empty_like if len(flat) else torch.zeros_like
             da, db = allocate(a), allocate(b)
             low = torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype)
-            xa = (shared[:, index*len(a):(index+1)*len(a)] if shared is not None
+            xa = (kept[index] if kept is not None else shared[:, index*len(a):(index+1)*len(a)] if shared is not None
                   else torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype))
             rotate = ctx.head_dim and index < 2
             for start in range(0, len(flat), step):
@@ -429,7 +442,7 @@ class _LoRAGroup(torch.autograd.Function):
                     base.input_gradient(signal, ac, bc, dx[start:stop], part_low, index > 0)
                 else:
                     _low_rank(signal, bc, part_low, transpose=False)
-                if shared is None:
+                if shared is None and kept is None:
                     _low_rank(flat[start:stop], ac, part_xa, transpose=True)
                 parameter_gradients(flat[start:stop], signal, da, db, part_low, part_xa, add=start > 0)
             results.extend((None, da, db, None))

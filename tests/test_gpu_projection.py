@@ -333,3 +333,31 @@ def test_shared_group_with_bf16_adapters():
     for a, b in zip(got, want):
         assert a.dtype == b.dtype
         assert ((a.float() - b.float()).norm() / b.float().norm()).item() < .03
+
+
+@pytest.mark.parametrize("count", [1, 3])
+def test_backward_reads_the_forward_xa(monkeypatch, count):
+    """With one tile over all rows the group keeps each projection's forward xa = x a^T and
+    the backward runs no rank-r GEMM on x again; its gradients equal those of the tiled
+    backward, which recomputes xa per tile as the reference does (linear.py:124-125)."""
+    from causal_tuner.kernels import linear
+    modules = [_projection(256, n, 32, seed=7 + i) for i, n in enumerate((256, 64, 64)[:count])]
+    x = torch.randn(512, 256, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    outputs = linear.project_group(modules, x)
+    signals = [torch.randn_like(out) for out in outputs]
+    params = [x, *(p for m in modules for p in (m.lora_A, m.lora_B))]
+    calls = []
+    for name in ("_shared_xa", "_low_rank"):
+        original = getattr(linear, name)
+        monkeypatch.setattr(linear, name, lambda *args, _f=original, _n=name, **kw: (
+            calls.append((_n, kw.get("transpose", True))), _f(*args, **kw))[1])
+    kept = torch.autograd.grad(outputs, params, signals)
+    monkeypatch.undo()
+    # no x [a_1; ...]^T and no x a^T in the backward (low = dy b would be transpose=False)
+    assert not [call for call in calls if call[1]], calls
+    tiled = linear.project_group(modules, x, 128)
+    recomputed = torch.autograd.grad(tiled, params, signals)
+    for out, again in zip(outputs, tiled):
+        assert torch.equal(out, again) or ((out.float() - again.float()).norm() / again.float().norm()).item() < 1e-2
+    for a, b in zip(kept, recomputed):
+        assert ((a.float() - b.float()).norm() / b.float().norm()).item() < 1e-2
