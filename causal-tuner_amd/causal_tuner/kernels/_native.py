@@ -79,6 +79,9 @@ EXPORTED = tuple(_SIGNATURES)
 _library = None
 
 
+ABI_VERSION = 6   # ct_abi_version() of the library these signatures describe
+
+
 def library_path():
     return os.environ.get("CAUSAL_TUNER_HIP_LIBRARY", DEFAULT_LIBRARY)
 
@@ -94,6 +97,9 @@ def library():
         for name, (restype, argtypes) in _SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype, fn.argtypes = restype, argtypes
+        if lib.ct_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"The HIP library {path} has ABI {lib.ct_abi_version()}, this binding needs "
+                               f"{ABI_VERSION}; rebuild it with `python causal-tuner_amd/build.py`")
         _library = lib
     return _library
 
