@@ -377,6 +377,13 @@ def skinny_measure(device, shapes=((6144, 24576), (24576, 6144)), rows_list=(16,
     return results
 
 
+# The reference's runtime option mlp_cache_budget_bytes (training/execution.py:65-66):
+# the C4 step keeps every layer's gate/up outputs and xa (138 MB per layer at 4096 tokens,
+# 3.3 GB for 24), which MI355X's 288 GB holds; the reference's own policy enables the same
+# cache per layer when memory allows (modeling/model.py:227-237).
+MLP_CACHE_BYTES = 16 << 30
+
+
 def c4_measure(device, steps=5, warmup=2):
     """C4: one full LoRA training step of the 24-layer MQA decoder (d 2048, 16 x 128 query
     heads, one KV head, I 8192, vocab 49152, partial RoPE theta 1e4, NF4 frozen bases, rank
@@ -408,7 +415,7 @@ def c4_measure(device, steps=5, warmup=2):
                      betas=(0.9, 0.999), eps=1e-8)
 
     def step():
-        loss = model.loss(ids, targets, weights, records)
+        loss = model.loss(ids, targets, weights, records, mlp_cache_bytes=MLP_CACHE_BYTES)
         loss.backward()
         torch.nn.utils.clip_grad_norm_(params, 1.0, foreach=True)
         opt.step()
@@ -431,6 +438,8 @@ def c4_measure(device, steps=5, warmup=2):
               "ms_per_step": round(ms, 3), "steps": steps, "warmup": warmup,
               "trainable_params": sum(p.numel() for p in params), "loss": round(float(loss.detach()), 4),
               "attention": "torch SDPA (memory-efficient backend), causal per record",
+              "mlp_cache": {"budget_GiB": MLP_CACHE_BYTES / 2**30,
+                            "layers": sum(layer.mlp.cache_intermediates for layer in model.layers)},
               "peak_mem_GiB": round(torch.cuda.max_memory_allocated() / 2**30, 2)}
     del model, opt, params
     torch.cuda.empty_cache()

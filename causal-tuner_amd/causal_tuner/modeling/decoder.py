@@ -9,9 +9,12 @@ residual, the MLP is `tiled_lora_mlp` with the residual; RMSNorm runs the HIP ke
 and the loss is `projection_loss` over the supervised rows. Attention is PyTorch-ROCm's
 scaled-dot-product attention (memory-efficient backend, flash as the deterministic
 choice), causal within each packed record, with the
-single key/value head broadcast to the query heads. Not here (the reference's runtime
-options): gradient checkpointing, activation offload, attention and MLP caches,
-trainable embeddings or head, tied weights.
+single key/value head broadcast to the query heads. The MLP cache budget
+(`mlp_cache_bytes`) is the reference's runtime option: layers from the last one back keep
+their gate/up outputs and xa while the budget lasts (modeling/model.py:227-237), so their
+backward skips the gate/up recompute. Not here (the reference's other runtime options):
+gradient checkpointing, activation offload, the attention cache, trainable embeddings or
+head, tied weights.
 """
 
 from dataclasses import dataclass
@@ -150,15 +153,28 @@ class Decoder(nn.Module):
             if isinstance(module, Projection) and module.weight is not None:
                 module.install_nf4(module.weight, module.weight.device)
 
-    def hidden(self, ids, records):
+    def plan_mlp_cache(self, rows, budget):
+        """Cache mode per layer, from the last layer back while `budget` bytes last
+        (modeling/model.py:227-237); returns the bytes retained."""
+        remaining, retained = budget if torch.is_grad_enabled() else 0, 0
+        for layer in reversed(self.layers):
+            cost = layer.mlp.cache_bytes(rows) if remaining else 0
+            layer.mlp.cache_intermediates = bool(cost and cost <= remaining)
+            if layer.mlp.cache_intermediates:
+                remaining -= cost
+                retained += cost
+        return retained
+
+    def hidden(self, ids, records, *, mlp_cache_bytes=0):
         positions = record_positions(records, ids.device)
         cosine, sine = rotary_values(positions, self.config, torch.bfloat16)
         x = self.embed_tokens(ids)
+        self.plan_mlp_cache(ids.numel() if ids.is_cuda else 0, mlp_cache_bytes)
         for layer in self.layers:
             x = layer(x, cosine, sine, records)
         return self.norm(x)
 
-    def loss(self, ids, targets, weights, records, *, token_budget=128):
+    def loss(self, ids, targets, weights, records, *, token_budget=128, mlp_cache_bytes=0):
         from ..kernels.loss import projection_loss
-        return projection_loss(self.hidden(ids, records), self.lm_head.weight, targets, weights,
-                               token_budget=token_budget)
+        return projection_loss(self.hidden(ids, records, mlp_cache_bytes=mlp_cache_bytes), self.lm_head.weight,
+                               targets, weights, token_budget=token_budget)

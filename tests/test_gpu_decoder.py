@@ -129,3 +129,27 @@ def test_decoder_adamw_step_lowers_the_loss():
         opt.step()
         opt.zero_grad(set_to_none=True)
     assert float(model.loss(ids[None], targets[None], weights[None], records).detach()) < first
+
+
+def test_mlp_cache_budget_gives_identical_loss_and_gradients():
+    """With an MLP cache budget (the reference's mlp_cache_budget_bytes, assigned from the
+    last layer back: modeling/model.py:227-237) the cached layers' backward reads the
+    forward's gate/up and xa instead of recomputing them: the loss and every LoRA gradient
+    equal the uncached step bit for bit. A budget for one layer caches only the last."""
+    model = _tiny()
+    ids, targets, weights, records = _batch(model)
+    rows = ids.numel()
+    one = model.layers[0].mlp.cache_bytes(rows)
+    results = []
+    for budget, cached in ((0, [False, False]), (one, [False, True]), (4 * one, [True, True])):
+        model.zero_grad(set_to_none=True)
+        loss = model.loss(ids[None], targets[None], weights[None], records, token_budget=16, mlp_cache_bytes=budget)
+        assert [layer.mlp.cache_intermediates for layer in model.layers] == cached
+        loss.backward()
+        results.append((loss.detach().clone(), {n: p.grad.clone() for n, p in model.named_parameters()
+                                                if p.grad is not None}))
+    for loss, grads in results[1:]:
+        assert torch.equal(loss, results[0][0])
+        assert grads.keys() == results[0][1].keys()
+        for name, grad in grads.items():
+            assert torch.equal(grad, results[0][1][name]), name
