@@ -167,16 +167,19 @@ class _TiledLoRAMLP(torch.autograd.Function):
             xa = [buffer[:len(part)] for buffer in low_inputs]
             low = [low_grad[:len(part), :len(a)] for a, _ in adapters]
             if ctx.cache:
-                # The activation backward overwrites its tile buffers: copy only this tile so
-                # the saved values survive a repeated backward.
-                gate.copy_(saved[0][start:start+len(part)])
-                up.copy_(saved[1][start:start+len(part)])
                 xa[:2] = [value[start:start+len(part)] for value in saved[2:]]
             else:
                 _gate_up(part, matrices, adapters, gate, up, xa, stack)
             input_gradient(dy, matrices[2], *adapters[2], dh, low[2])
-            # Reuse the three wide tile buffers: (gate, up, dh) -> (d gate, d up, hidden).
-            hidden = activation(gate, up, dh)
+            if ctx.cache:
+                # The saved gate/up stay untouched (a repeated backward reads them again):
+                # the activation backward reads them and writes d gate, d up into the tile
+                # buffers and hidden over dh, where the reference copies the tile first.
+                _silu(saved[0][start:start+len(part)], saved[1][start:start+len(part)], dh, gate, up, True, True)
+                hidden = dh
+            else:
+                # Reuse the three wide tile buffers: (gate, up, dh) -> (d gate, d up, hidden).
+                hidden = activation(gate, up, dh)
             _low_rank(hidden, adapters[2][0], xa[2], transpose=True)
             parameter_gradients(hidden, dy, *gradients[2], low[2], xa[2], add=start > 0)
             for index, signal in enumerate((gate, up)):
