@@ -82,13 +82,20 @@ def build_layer(device, tokens=T, seed=0):
     return modules, inputs, grads
 
 
+# Device memory the C3 step lets each projection group keep between its forward and
+# backward (linear.projection_budget): with it every group runs its 8192 rows as one tile
+# and keeps its forward xa (4 MB per projection) instead of recomputing it per 4096-row tile.
+PROJECTION_BUDGET = 1 << 30
+
+
 def layer_step(modules, inputs, grads):
-    from causal_tuner.kernels.linear import project_group
+    from causal_tuner.kernels.linear import project_group, projection_budget
     m = modules
-    q, k, v = project_group((m["q"], m["k"], m["v"]), inputs["x"])
-    o, = project_group((m["o"],), inputs["y"])
-    gate, up = project_group((m["gate"], m["up"]), inputs["x2"])
-    down, = project_group((m["down"],), inputs["h"])
+    with projection_budget(PROJECTION_BUDGET):
+        q, k, v = project_group((m["q"], m["k"], m["v"]), inputs["x"])
+        o, = project_group((m["o"],), inputs["y"])
+        gate, up = project_group((m["gate"], m["up"]), inputs["x2"])
+        down, = project_group((m["down"],), inputs["h"])
     outputs = (q, k, v, o, gate, up, down)
     wrt = [inputs[key] for key in ("x", "y", "x2", "h")]
     for name in ("q", "k", "v", "o", "gate", "up", "down"):
@@ -415,7 +422,8 @@ def c4_measure(device, steps=5, warmup=2):
                      betas=(0.9, 0.999), eps=1e-8)
 
     def step():
-        loss = model.loss(ids, targets, weights, records, mlp_cache_bytes=MLP_CACHE_BYTES)
+        loss = model.loss(ids, targets, weights, records, mlp_cache_bytes=MLP_CACHE_BYTES,
+                          projection_bytes=PROJECTION_BUDGET)
         loss.backward()
         torch.nn.utils.clip_grad_norm_(params, 1.0, foreach=True)
         opt.step()

@@ -20,6 +20,8 @@ except in `accumulate`, which keeps the reference's addmm for operands that are 
 (the fp32 projection loss uses it; linear.py:22-24).
 """
 
+import contextlib
+import contextvars
 import ctypes
 
 import torch
@@ -148,13 +150,6 @@ def group_factors(parameters, count, dtype, x, shared=None):
         outputs = [stack[i*r:(i+1)*r] if j == 0 and i < shared else None for i in range(count) for j in (0, 1)]
         return cast_all(tensors, dtype, outputs), stack
     return cast_all(tensors, dtype), None
-
-
-def _shared_xa(flat, stack):
-    """x [a_1; a_2; ...]^T for a group: one ct_gemm, column slice i is projection i's xa."""
-    xa = torch.empty((len(flat), len(stack)), dtype=flat.dtype, device=flat.device)
-    _low_rank(flat, stack, xa, transpose=True)
-    return xa
 
 
 def materialize(weight, state, dtype):
@@ -348,53 +343,91 @@ class _Base:
             _input_gradient(dy, self.weight, self.state, a, b, dx, low, add)
 
 
-class _LoRAGroup(torch.autograd.Function):
-    """Projections sharing one input (linear.py:59-130). Saves the input and parameters and,
-    when one tile covers all rows, each projection's forward xa = x a^T ([rows, r], 4 MB at
-    8192 x 256 in bf16), which the reference recomputes in the backward (linear.py:124-125):
-    the backward then reads the same values instead of running the rank-r GEMMs again.
+# Rows per tile of a projection group called without a tile: the reference's bound
+# (linear.py:63), which keeps every row-proportional workspace at most [4096, ...] wide.
+DEFAULT_TILE = 4096
+_KEEP_BUDGET = contextvars.ContextVar("causal_tuner_projection_budget", default=0)
 
-    Without an explicit tile the backward runs each projection over all rows at once (the
-    rank-r workspaces are [rows, r]); an explicit tile bounds them as in the reference and
-    keeps its recompute."""
+
+@contextlib.contextmanager
+def projection_budget(nbytes):
+    """Let projection groups called without a tile inside this block spend up to `nbytes`
+    of device memory on row-proportional state: when a group's whole input fits, it runs
+    all rows as one tile and keeps each projection's forward xa = x a^T for its backward
+    instead of recomputing it. The default budget is 0: 4096-row tiles and nothing saved
+    but the input and the parameters, as in the reference (linear.py:59-130). The budget
+    is read when the forward runs; the backward follows the forward's choice."""
+    if nbytes < 0:
+        raise ValueError("The projection budget must be non-negative")
+    token = _KEEP_BUDGET.set(int(nbytes))
+    try:
+        yield
+    finally:
+        _KEEP_BUDGET.reset(token)
+
+
+def group_row_bytes(parameters, count, element, head_dim):
+    """Device bytes per input row that one whole-input tile of a group holds across its
+    forward and backward: every kept xa, the backward's [rows, r] gradient product and,
+    with rotary outputs, the inverse-rotation scratch of a q or k gradient."""
+    ranks = [len(parameters[4*i+1]) for i in range(count)]
+    widths = [len(parameters[4*i+2]) for i in range(min(count, 2))] if head_dim else [0]
+    return element * (sum(ranks) + max(ranks, default=0) + max(widths, default=0))
+
+
+def _plan_rows(rows, tile, budget, row_bytes):
+    """(rows per tile, keep xa): an explicit tile is the reference's tiled path; without one
+    the whole input is one tile when the budget covers it, else DEFAULT_TILE rows."""
+    if tile:
+        return tile, False
+    if 0 < rows and rows * row_bytes <= budget:
+        return rows, True
+    return DEFAULT_TILE, False
+
+
+class _LoRAGroup(torch.autograd.Function):
+    """Projections sharing one input (linear.py:59-130), in tiles of rows.
+
+    Projections of one rank that read the same input get their xa = x a_i^T from one GEMM
+    over the stacked factors per tile (`group_factors`). Under a projection budget that
+    covers the whole input (`projection_budget`) the group runs one tile and saves each
+    projection's xa for the backward; otherwise it saves only the input and the
+    parameters and the backward recomputes xa tile by tile. The backward visits tiles in
+    order and, inside a tile, the projections in order, so dx accumulates over the
+    projections (add=index>0) and dA/dB over the tiles (add=start>0) in the reference's
+    sequence."""
 
     @staticmethod
     def forward(ctx, x, dtype, tile, states, cosine, sine, head_dim, residual, *parameters):
-        ctx.dtype, ctx.tile, ctx.states = dtype, tile, states
-        ctx.head_dim = head_dim
+        count = len(states)
         flat = x.reshape(-1, x.shape[-1]).to(dtype)
-        outputs = []
-        step = tile or max(len(flat), 1)
-        rows = min(step, len(flat))
-        factors, stack = group_factors(parameters, len(states), dtype, x)
-        # One tile over all rows: the projections' xa come from one GEMM over the stacked
-        # factors (the same products; the fp32 sums may be split differently than in
-        # separate launches, so a value can differ by one bf16 rounding).
-        shared = _shared_xa(flat, stack) if stack is not None and 0 < len(flat) <= step else None
-        kept = []   # each projection's xa over all rows, for the backward
-        for index, state in enumerate(states):
-            weight, a, b, bias = parameters[index*4:index*4+4]
-            base, ac, bc = _Base(weight, state, dtype), factors[2*index], factors[2*index+1]
-            bias = None if bias is None else bias.to(dtype)
-            out = torch.empty((len(flat), base.rows), device=x.device, dtype=dtype)
-            if shared is not None:
-                r = len(a)
-                kept.append(shared[:, index*r:(index+1)*r])
-                base.forward(flat, ac, bc, bias, out, kept[-1], xa_given=True)
-            else:
-                low = torch.empty((rows, len(a)), device=x.device, dtype=dtype)
-                for start in range(0, len(flat), step):
-                    part = flat[start:start+step]
-                    base.forward(part, ac, bc, bias, out[start:start+step], low[:len(part)])
-                kept.append(low)
-                del low
-            outputs.append(out.reshape(*x.shape[:-1], base.rows))
-            del base, ac, bc
-        if not 0 < len(flat) <= step:
-            kept = []   # tiled (xa of the last tile only) or empty: the backward recomputes
+        element = torch.empty((), dtype=dtype).element_size()
+        step, keep = _plan_rows(len(flat), tile, _KEEP_BUDGET.get(),
+                                group_row_bytes(parameters, count, element, head_dim))
+        ctx.dtype, ctx.states, ctx.head_dim, ctx.step = dtype, states, head_dim, step
+        factors, stack = group_factors(parameters, count, dtype, x)
+        bases = [_Base(parameters[4*i], state, dtype) for i, state in enumerate(states)]
+        biases = [None if parameters[4*i+3] is None else parameters[4*i+3].to(dtype) for i in range(count)]
+        outputs = [torch.empty((len(flat), base.rows), device=x.device, dtype=dtype) for base in bases]
+        ranks = [len(parameters[4*i+1]) for i in range(count)]
+        span = min(step, len(flat))
+        # xa of every projection for the rows of one tile (all rows when kept), as column
+        # slices of one buffer so a stacked GEMM fills them together.
+        xa = torch.empty((len(flat) if keep else span, sum(ranks)), device=x.device, dtype=dtype)
+        columns = [xa[:, sum(ranks[:i]):sum(ranks[:i+1])] for i in range(count)]
+        for start in range(0, len(flat), step):
+            part = flat[start:start+step]
+            rows = slice(start, start+len(part)) if keep else slice(0, len(part))
+            if stack is not None:
+                _low_rank(part, stack, xa[rows], transpose=True)
+            for index, base in enumerate(bases):
+                base.forward(part, factors[2*index], factors[2*index+1], biases[index],
+                             outputs[index][start:start+len(part)], columns[index][rows], xa_given=stack is not None)
+        kept = columns if keep else []
         ctx.kept = len(kept)
         ctx.save_for_backward(x, cosine, sine, *parameters, *kept)
-        del factors, stack, shared, kept
+        del factors, stack, bases, xa, columns, kept
+        outputs = [out.reshape(*x.shape[:-1], out.shape[1]) for out in outputs]
         if head_dim:
             from .core_cuda import rotate_owned_qk
             rotate_owned_qk(outputs[0], outputs[1], cosine, sine, head_dim)
@@ -404,49 +437,53 @@ class _LoRAGroup(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grad_outputs):
-        x, cosine, sine, *parameters = ctx.saved_tensors
-        kept = parameters[len(parameters)-ctx.kept:] if ctx.kept else None
-        parameters = parameters[:len(parameters)-ctx.kept]
+        x, cosine, sine, *rest = ctx.saved_tensors
+        count = len(ctx.states)
+        parameters, kept = rest[:4*count], rest[4*count:]
         flat = x.reshape(-1, x.shape[-1]).to(ctx.dtype)
         dx = torch.empty_like(flat) if ctx.needs_input_grad[0] else None
         if ctx.head_dim:
             cosine, sine = (value.reshape(-1, value.shape[-1]) for value in (cosine, sine))
-        step = ctx.tile or max(len(flat), 1)
-        rows = min(step, len(flat))
-        rotary = (torch.empty(rows*max(len(b) for b in parameters[2:8:4]), device=x.device, dtype=ctx.dtype)
-                  if ctx.head_dim else None)
-        results = []
-        factors, stack = group_factors(parameters, len(ctx.states), ctx.dtype, x)
-        shared = (_shared_xa(flat, stack) if kept is None and stack is not None and 0 < len(flat) <= step
-                  else None)
-        for index, (state, grad) in enumerate(zip(ctx.states, grad_outputs)):
-            weight, a, b, _ = parameters[index*4:index*4+4]
-            base = _Base(weight, state, ctx.dtype) if dx is not None else None
-            ac, bc = factors[2*index], factors[2*index+1]
-            dy = grad.reshape(-1, grad.shape[-1]).to(ctx.dtype)
-            allocate = torch.empty_like if len(flat) else torch.zeros_like
-            da, db = allocate(a), allocate(b)
-            low = torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype)
-            xa = (kept[index] if kept is not None else shared[:, index*len(a):(index+1)*len(a)] if shared is not None
-                  else torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype))
-            rotate = ctx.head_dim and index < 2
-            for start in range(0, len(flat), step):
-                stop = start+step
-                signal = dy[start:stop]
-                if rotate:
-                    from .core_cuda import inverse_rope_tile
-                    target = rotary[:signal.numel()].view_as(signal)
-                    signal = inverse_rope_tile(signal, cosine[start:stop], sine[start:stop], ctx.head_dim, target)
-                part_low, part_xa = low[:len(signal)], xa[:len(signal)]
-                if dx is not None:
-                    base.input_gradient(signal, ac, bc, dx[start:stop], part_low, index > 0)
+        step, span = ctx.step, min(ctx.step, len(flat))
+        factors, stack = group_factors(parameters, count, ctx.dtype, x)
+        bases = [_Base(parameters[4*i], state, ctx.dtype) if dx is not None else None
+                 for i, state in enumerate(ctx.states)]
+        ranks = [len(parameters[4*i+1]) for i in range(count)]
+        signals = [grad.reshape(-1, grad.shape[-1]).to(ctx.dtype) for grad in grad_outputs]
+        allocate = torch.empty_like if len(flat) else torch.zeros_like
+        gradients = [(allocate(parameters[4*i+1]), allocate(parameters[4*i+2])) for i in range(count)]
+        low = torch.empty((span, max(ranks)), device=x.device, dtype=ctx.dtype)
+        xa = None if kept else torch.empty((span, sum(ranks)), device=x.device, dtype=ctx.dtype)
+        rotated = min(count, 2) if ctx.head_dim else 0
+        scratch = (torch.empty(span * max(signals[i].shape[1] for i in range(rotated)), device=x.device,
+                               dtype=ctx.dtype) if rotated else None)
+        for start in range(0, len(flat), step):
+            part = flat[start:start+step]
+            if not kept:
+                if stack is not None:
+                    _low_rank(part, stack, xa[:len(part)], transpose=True)
                 else:
-                    _low_rank(signal, bc, part_low, transpose=False)
-                if shared is None and kept is None:
-                    _low_rank(flat[start:stop], ac, part_xa, transpose=True)
-                parameter_gradients(flat[start:stop], signal, da, db, part_low, part_xa, add=start > 0)
-            results.extend((None, da, db, None))
-            del base, ac, bc, dy
+                    for index in range(count):
+                        columns = slice(sum(ranks[:index]), sum(ranks[:index+1]))
+                        _low_rank(part, factors[2*index], xa[:len(part), columns], transpose=True)
+            for index in range(count):
+                a, b = factors[2*index], factors[2*index+1]
+                signal = signals[index][start:start+len(part)]
+                if index < rotated:
+                    from .core_cuda import inverse_rope_tile
+                    target = scratch[:signal.numel()].view_as(signal)
+                    signal = inverse_rope_tile(signal, cosine[start:start+len(part)], sine[start:start+len(part)],
+                                               ctx.head_dim, target)
+                grad_low = low[:len(part), :ranks[index]]
+                if dx is not None:
+                    bases[index].input_gradient(signal, a, b, dx[start:start+len(part)], grad_low, index > 0)
+                else:
+                    _low_rank(signal, b, grad_low, transpose=False)
+                inputs = (kept[index][start:start+len(part)] if kept else
+                          xa[:len(part), sum(ranks[:index]):sum(ranks[:index+1])])
+                parameter_gradients(part, signal, *gradients[index], grad_low, inputs, add=start > 0)
+        del bases, factors, stack
+        results = [value for da, db in gradients for value in (None, da, db, None)]
         residual_grad = grad_outputs[0] if ctx.needs_input_grad[7] else None
         return (None if dx is None else dx.reshape_as(x).to(x.dtype), None, None, None, None, None, None,
                 residual_grad, *results)

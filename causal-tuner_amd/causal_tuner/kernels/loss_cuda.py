@@ -1,123 +1,157 @@
-"""Fused weighted cross-entropy and the tiled projection loss on gfx950 (the reference's
-kernels/loss_cuda.py).
+"""Weighted cross-entropy and the row-tiled projection loss on gfx950.
 
-`weighted_ce` (loss_cuda.py:11-70) keeps the reference's signature and contract: per-row
-weighted losses, and with `gradient=True` the logits overwritten in place by the weighted
-softmax derivative. It runs the HIP kernel ct_weighted_ce (4096-column splits per row as
-the reference's _statistics/_finish, fixed reduction order) with its own workspace; the
-reference's `partials` argument is accepted and not needed. `FusedProjectionLoss` (loss_cuda.py:81-162) drives it tile by tile.
+Interface of the reference's kernels/loss_cuda.py: `weighted_ce` (11-70) and
+`FusedProjectionLoss` (81-162).
+
+`weighted_ce` writes per-row weighted losses and, with `gradient=True`, overwrites the
+logits with the weighted softmax derivative; it runs the HIP kernel ct_weighted_ce (two
+launches over 4096-column splits, fixed reduction order). Its `partials` argument, the
+reference's split-statistics buffer, is accepted for callers that pass it; the HIP kernel
+keeps its statistics in its own workspace.
+
+`FusedProjectionLoss` computes the loss and both gradients in its forward, tile by tile
+over the supervised rows (`_SupervisedRows`), with one logits buffer for every tile:
+logits = x head^T (the BLAS library's GEMM through torch.mm), the fused CE over them, then
+d head += derivative^T x (`linear.accumulate`: fp32 output) and d hidden = derivative head
+for the tile's rows. Its backward only scales the cached gradients.
 """
 
 import torch
 
 from . import _native
 
-_CE_ROWS = 65535  # rows per ct_weighted_ce call
+_CE_ROWS = 65535  # rows per ct_weighted_ce call (the kernel's grid limit)
 
 
 def weighted_ce(logits, targets, weights, *, gradient, loss=None, partials=None):
-    """Write per-row weighted losses and optionally overwrite logits with derivatives."""
     rows, vocab = logits.shape
     if not logits.is_cuda:
         raise ValueError("weighted_ce expects device tensors")
     if logits.stride(1) != 1:
         raise ValueError("weighted_ce needs unit-stride logits rows")
-    if loss is None:
-        loss = torch.empty(rows, device=logits.device, dtype=torch.float32)
-    targets = targets.to(torch.int64).contiguous()
-    weights = weights.to(torch.float32).contiguous()
+    loss = torch.empty(rows, device=logits.device, dtype=torch.float32) if loss is None else loss
+    labels = targets.to(torch.int64).contiguous()
+    scale = weights.to(torch.float32).contiguous()
     lib = _native.library()
-    for start in range(0, rows, _CE_ROWS):
-        part = min(_CE_ROWS, rows - start)
-        workspace = torch.empty(max(lib.ct_weighted_ce_workspace(part, vocab), 1), dtype=torch.uint8,
-                                device=logits.device)
+    code, pitch, stream = _native.dtype_code(logits.dtype), logits.stride(0), _native.stream_of(logits)
+    for first in range(0, rows, _CE_ROWS):
+        count = min(_CE_ROWS, rows - first)
+        scratch = torch.empty(max(lib.ct_weighted_ce_workspace(count, vocab), 1), dtype=torch.uint8,
+                              device=logits.device)
+        window = slice(first, first + count)
         with _native.device_of(logits):
-            status = lib.ct_weighted_ce(
-                _native.ptr(logits[start:start + part]), _native.dtype_code(logits.dtype), part, vocab,
-                logits.stride(0), _native.ptr(targets[start:start + part]), _native.ptr(weights[start:start + part]),
-                _native.ptr(loss[start:start + part]), int(bool(gradient)), _native.ptr(workspace), workspace.numel(),
-                _native.stream_of(logits))
+            status = lib.ct_weighted_ce(_native.ptr(logits[window]), code, count, vocab, pitch,
+                                        _native.ptr(labels[window]), _native.ptr(scale[window]),
+                                        _native.ptr(loss[window]), int(bool(gradient)), _native.ptr(scratch),
+                                        scratch.numel(), stream)
         _native.check(status, "ct_weighted_ce")
     return loss
 
 
-class FusedProjectionLoss(torch.autograd.Function):
-    """Projection + weighted CE over tiles of at most `tile` supervised rows, gradients
-    computed once in the forward (the reference's kernels/loss_cuda.py:81-162).
+class _SupervisedRows:
+    """The supervised rows of a flattened batch, visited in tiles of at most `tile` rows.
 
-    Per tile: logits = x head^T (the BLAS library's GEMM, as in the reference), then the
-    HIP kernel ct_weighted_ce writes the weighted losses and overwrites the logits with the
-    weighted softmax derivative; dHead += derivative^T x runs in `accumulate` (fp32 output;
-    the HIP GEMM for bf16 operands); dHidden = derivative head goes to its rows. The
-    backward only scales the cached gradients. One logits workspace serves every tile."""
+    An interval (a slice) is read through views and written in place; scattered rows (an
+    index tensor) are gathered into staging buffers that every tile reuses and their
+    gradients are scattered back with index_copy_."""
+
+    def __init__(self, active, hidden, targets, weights, tile):
+        self.active, self.tile = active, tile
+        self.interval = isinstance(active, slice)
+        self.count = (active.stop - active.start) if self.interval else len(active)
+        self.hidden, self.targets, self.weights = hidden, targets, weights
+        rows = min(tile, self.count)
+        if not self.interval and rows:
+            self.staged = (hidden.new_empty((rows, hidden.shape[-1])), targets.new_empty(rows),
+                           weights.new_empty(rows))
+
+    def __iter__(self):
+        """(offset of the tile among the supervised rows, row selector, size)."""
+        for offset in range(0, self.count, self.tile):
+            size = min(self.tile, self.count - offset)
+            if self.interval:
+                first = self.active.start + offset
+                yield offset, slice(first, first + size), size
+            else:
+                yield offset, self.active[offset:offset + size], size
+
+    def gather(self, where, size):
+        """(hidden rows, targets, weights) of one tile."""
+        if self.interval:
+            return self.hidden[where], self.targets[where], self.weights[where]
+        rows, labels, scale = (buffer[:size] for buffer in self.staged)
+        for source, buffer in ((self.hidden, rows), (self.targets, labels), (self.weights, scale)):
+            torch.index_select(source, 0, where, out=buffer)
+        return rows, labels, scale
+
+    def clear_unsupervised(self, grad, holds_hidden):
+        """Zero the gradient rows that no tile wrote. Rows outside an interval are always
+        cleared; between scattered rows only when `grad` still holds the hidden values
+        (fresh gradients of scattered rows start from zeros)."""
+        if self.interval:
+            grad[:self.active.start].zero_()
+            grad[self.active.stop:].zero_()
+        elif holds_hidden and self.count != len(grad):
+            grad.masked_fill_(~(self.weights > 0)[:, None], 0)
+
+
+class FusedProjectionLoss(torch.autograd.Function):
+    """Sum over supervised rows of weight * CE(x head^T, target), gradients computed in the
+    forward. `reuse` hands d hidden the storage of `hidden` (which must be an exclusive,
+    contiguous non-leaf tensor): it is marked dirty and returned as the second output."""
 
     @staticmethod
-    def forward(ctx, hidden, head, targets, weights, tile, dtype, reuse_hidden, active):
+    def forward(ctx, hidden, head, targets, weights, tile, dtype, reuse, active):
         from .linear import accumulate
-        from .loss import row_count
         h = hidden.reshape(-1, hidden.shape[-1])
-        t, w = targets.flatten(), weights.flatten()
-        count = row_count(active)
-        contiguous = isinstance(active, slice)
-        reuse_hidden = reuse_hidden and ctx.needs_input_grad[0]
-        allocate = torch.empty_like if contiguous else torch.zeros_like
-        dh = (h if reuse_hidden else allocate(h)) if ctx.needs_input_grad[0] else None
-        dw = (torch.empty_like(head) if count else torch.zeros_like(head)) if ctx.needs_input_grad[1] else None
-        losses = torch.empty(count, device=hidden.device, dtype=torch.float32)
-        rows = min(tile, count)
-        # dHidden rows can be written straight into place when they form one interval and
-        # the destination has the compute dtype.
-        direct = contiguous and dh is not None and dh.dtype == dtype
-        if rows:
+        rows = _SupervisedRows(active, h, targets.flatten(), weights.flatten(), tile)
+        need_dh, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        reuse = reuse and need_dh
+        if not need_dh:
+            dh = None
+        elif reuse:
+            dh = h
+        else:
+            dh = torch.empty_like(h) if rows.interval else torch.zeros_like(h)
+        dw = None if not need_dw else (torch.empty_like(head) if rows.count else torch.zeros_like(head))
+        losses = torch.empty(rows.count, device=hidden.device, dtype=torch.float32)
+        if rows.count:
             matrix = head.to(dtype)
-            workspace = torch.empty((rows, len(matrix)), device=hidden.device, dtype=dtype)
-            if not contiguous:
-                inputs = h.new_empty((rows, h.shape[-1]))
-                labels, factors = t.new_empty(rows), w.new_empty(rows)
-            signals = (torch.empty((rows, h.shape[-1]), device=hidden.device, dtype=dtype)
-                       if dh is not None and not direct else None)
-            # The reference's split-statistics workspace, kept so that callers (and tests)
-            # that inspect weighted_ce's arguments see the same contract.
+            span = min(tile, rows.count)
+            logits_buffer = torch.empty((span, len(matrix)), device=hidden.device, dtype=dtype)
             splits = -(-len(matrix) // 4096)
-            partials = (torch.empty((rows, splits), device=hidden.device, dtype=torch.float32)
-                        if splits > 1 else losses)
-        for start in range(0, count, tile):
-            size = min(tile, count - start)
-            if contiguous:
-                indices = slice(active.start + start, active.start + start + size)
-                x, target, weight = h[indices].to(dtype), t[indices], w[indices]
-            else:
-                indices = active[start:start + size]
-                torch.index_select(h, 0, indices, out=inputs[:size])
-                torch.index_select(t, 0, indices, out=labels[:size])
-                torch.index_select(w, 0, indices, out=factors[:size])
-                x, target, weight = inputs[:size].to(dtype), labels[:size], factors[:size]
-            logits = workspace[:size]
-            torch.mm(x, matrix.T, out=logits)
-            weighted_ce(logits, target, weight, gradient=dh is not None or dw is not None,
-                        loss=losses[start:start + size], partials=partials[:size])
-            # With reuse, dHidden's rows are x's storage: the head gradient reads x first.
-            if dw is not None:
-                accumulate(dw, logits.T, x, add=start > 0)
-            if dh is not None:
-                if direct:
-                    torch.mm(logits, matrix, out=dh[indices])
+            statistics = (torch.empty((span, splits), device=hidden.device, dtype=torch.float32)
+                          if splits > 1 else losses)
+            # d hidden goes straight into its rows when they are an interval of the compute
+            # dtype; otherwise through a staging buffer.
+            in_place = rows.interval and dh is not None and dh.dtype == dtype
+            staging = (torch.empty((span, h.shape[-1]), device=hidden.device, dtype=dtype)
+                       if dh is not None and not in_place else None)
+            for offset, where, size in rows:
+                inputs, labels, scale = rows.gather(where, size)
+                x = inputs.to(dtype)
+                logits = logits_buffer[:size]
+                torch.mm(x, matrix.T, out=logits)
+                weighted_ce(logits, labels, scale, gradient=dh is not None or dw is not None,
+                            loss=losses[offset:offset + size], partials=statistics[:size])
+                # x may be a view of hidden's storage, which d hidden overwrites under reuse:
+                # the head gradient reads it first.
+                if dw is not None:
+                    accumulate(dw, logits.T, x, add=offset > 0)
+                if dh is None:
+                    continue
+                if in_place:
+                    torch.mm(logits, matrix, out=dh[where])
+                    continue
+                product = staging[:size]
+                torch.mm(logits, matrix, out=product)
+                if rows.interval:
+                    dh[where].copy_(product)
                 else:
-                    torch.mm(logits, matrix, out=signals[:size])
-                    if contiguous:
-                        dh[indices].copy_(signals[:size])
-                    else:
-                        dh.index_copy_(0, indices, signals[:size].to(dh.dtype))
-        if dh is not None and contiguous:
-            if active.start:
-                dh[:active.start].zero_()
-            if active.stop < len(h):
-                dh[active.stop:].zero_()
-        if reuse_hidden:
-            # Scattered supervision: active rows were gathered before their storage was
-            # overwritten; the remaining (unsupervised) rows still hold hidden values.
-            if not contiguous and count != len(h):
-                dh.view(len(w), -1).masked_fill_(~(w > 0)[:, None], 0)
+                    dh.index_copy_(0, where, product.to(dh.dtype))
+        if dh is not None:
+            rows.clear_unsupervised(dh, holds_hidden=reuse)
+        if reuse:
             ctx.mark_dirty(hidden)
             dh = hidden
         elif dh is not None:
@@ -126,16 +160,14 @@ class FusedProjectionLoss(torch.autograd.Function):
             ctx.mark_non_differentiable(dh)
         ctx.set_materialize_grads(False)
         ctx.save_for_backward(dh, dw)
-        # Returning the consumed input lets autograd see its in-place change.
         return losses.sum(), dh
 
     @staticmethod
-    def backward(ctx, upstream, unused):
+    def backward(ctx, upstream, _unused):
         dh, dw = ctx.saved_tensors
-        # Unit upstream (the training call) returns the cached gradients; any other scale
-        # makes new tensors, so the cache stays valid for a repeated backward.
-        scale = float(upstream)
-        if scale != 1:
+        # The training call's unit upstream returns the cached gradients themselves; any
+        # other scale makes new tensors, so a repeated backward still finds them intact.
+        if float(upstream) != 1:
             dh = None if dh is None else dh * upstream
             dw = None if dw is None else dw * upstream
         return dh, dw, None, None, None, None, None, None

@@ -1,212 +1,261 @@
-"""Tiled LoRA MLP with the SiLU-multiply and a graph-free analytic backward, on gfx950.
+"""The SwiGLU LoRA MLP as one autograd operator on gfx950.
 
-Same operator API as the reference's kernels/mlp_cuda.py: `activation` (10-35, the Triton
-`_activation` kernel, here `ct_silu_multiply`), `_SiLUMultiply` / `silu_multiply` (38-55),
-`_forward_into` (58-81), `_TiledLoRAMLP` (84-143) and `tiled_lora_mlp` (146-161). Gate, up and
-down are NF4-LoRA projections on the helpers of kernels/linear.py; a packed NF4 base stays
-packed below 512 rows (the GEMMs decode it in LDS) and is decoded once per call above.
+Interface of the reference's kernels/mlp_cuda.py: `activation` (10-35, its Triton
+`_activation`; here the HIP kernel `ct_silu_multiply`), `silu_multiply` (38-55),
+`_forward_into` (58-81), `_TiledLoRAMLP` (84-143) and `tiled_lora_mlp` (146-161).
+
+Design. One call builds an `_MLPProjections` view of the three projections: their frozen
+bases as the HIP GEMMs consume them (`linear._Base`: packed NF4 is decoded inside the entry
+points), their LoRA factors in the compute dtype (cast in one launch) and, when gate and up
+share a rank, the stacked [a_gate; a_up] whose single GEMM gives both xa. Rows are processed
+in tiles; per tile the forward is
+
+    xa_gate | xa_up = x [a_gate; a_up]^T         (one GEMM, or one per projection)
+    gate = x w_gate^T + xa_gate b_gate^T,  up = x w_up^T + xa_up b_up^T
+    h = bf16(silu(gate)) * up                     (ct_silu_multiply)
+    out = h w_down^T + (h a_down^T) b_down^T
+
+and the backward runs the reference's analytic sequence without an autograd graph: the down
+projection's input gradient dh, the SiLU backward in place of (gate, up, dh) giving (d gate,
+d up, h), then dA/dB of down from h and of gate/up from x, and dx accumulated over gate and
+up. In cache mode the forward keeps gate, up and their xa for every row and the backward
+reads them instead of recomputing the two GEMMs; the activation backward then writes its
+results into separate tile buffers so the kept values survive a repeated backward.
 """
 
 import torch
 
 from . import _native
-from .linear import _Base, group_factors, forward_linear, input_gradient, parameter_gradients, projection_parameters, _low_rank
+from .linear import _Base, _low_rank, forward_linear, group_factors, input_gradient, parameter_gradients, \
+    projection_parameters
 
 
-def _silu(gate, up, h, dg, du, backward, reconstruct):
-    tensors = [t for t in (gate, up, h, dg, du) if t is not None]
-    if not all(t.is_cuda and t.is_contiguous() and t.dtype == gate.dtype for t in tensors):
+# ----------------------------------------------------------------------------- SiLU x up
+def _silu_kernel(gate, up, hidden, d_gate, d_up, *, backward, reconstruct):
+    """ct_silu_multiply over whole contiguous tensors of one device dtype."""
+    operands = [t for t in (gate, up, hidden, d_gate, d_up) if t is not None]
+    if any(not (t.is_cuda and t.is_contiguous() and t.dtype == gate.dtype) for t in operands):
         raise ValueError("activation expects contiguous device tensors of one dtype")
     code = _native.dtype_code(gate.dtype)
     if code == _native.CT_F16:
         raise NotImplementedError("activation: the HIP kernel takes bfloat16 or float32")
     with _native.device_of(gate):
         status = _native.library().ct_silu_multiply(
-            _native.ptr(gate), _native.ptr(up), _native.ptr(h), _native.ptr(dg), _native.ptr(du), gate.numel(),
-            int(backward), int(reconstruct), code, _native.stream_of(gate))
+            _native.ptr(gate), _native.ptr(up), _native.ptr(hidden), _native.ptr(d_gate), _native.ptr(d_up),
+            gate.numel(), int(backward), int(reconstruct), code, _native.stream_of(gate))
     _native.check(status, "ct_silu_multiply")
 
 
 def activation(gate, up, gradient=None, *, out=None):
-    """h = dtype(silu(gate)) * up (reference mlp_cuda.py:28-35). With `gradient`, the
-    backward in place: gate <- d gate, up <- d up, gradient <- h."""
-    if gradient is not None:
-        out = gradient
-    elif out is None:
-        out = torch.empty_like(gate)
-    if gradient is not None:
-        _silu(gate, up, out, gate, up, True, True)
-    else:
-        _silu(gate, up, out, None, None, False, True)
-    return out
+    """Forward: returns h = dtype(silu(gate)) * up (in `out` when given). With `gradient`
+    (the upstream dh) the backward runs in place: gate becomes d gate, up becomes d up and
+    `gradient` is overwritten with h, which is returned."""
+    if gradient is None:
+        hidden = torch.empty_like(gate) if out is None else out
+        _silu_kernel(gate, up, hidden, None, None, backward=False, reconstruct=True)
+        return hidden
+    _silu_kernel(gate, up, gradient, gate, up, backward=True, reconstruct=True)
+    return gradient
 
 
 class _SiLUMultiply(torch.autograd.Function):
     @staticmethod
     def forward(ctx, gate, up):
-        gate, up = gate.contiguous(), up.contiguous()
-        ctx.save_for_backward(gate, up)
-        return activation(gate, up)
+        operands = gate.contiguous(), up.contiguous()
+        ctx.save_for_backward(*operands)
+        return activation(*operands)
 
     @staticmethod
     def backward(ctx, grad):
         gate, up = ctx.saved_tensors
-        dg, du = torch.empty_like(gate), torch.empty_like(up)
-        _silu(gate, up, grad.contiguous(), dg, du, True, False)
-        return dg, du
+        d_gate, d_up = torch.empty_like(gate), torch.empty_like(up)
+        _silu_kernel(gate, up, grad.contiguous(), d_gate, d_up, backward=True, reconstruct=False)
+        return d_gate, d_up
 
 
 def silu_multiply(gate, up):
     return _SiLUMultiply.apply(gate, up)
 
 
-def _bases(parameters, states, dtype):
-    return [_Base(parameters[4*i], state, dtype) for i, state in enumerate(states)]
+# ----------------------------------------------------------------------------- projections
+GATE, UP, DOWN = 0, 1, 2
 
 
+class _MLPProjections:
+    """Bases and compute-dtype factors of gate, up and down for one forward or backward."""
+
+    def __init__(self, parameters, states, dtype, x):
+        self.dtype, self.device = dtype, x.device
+        self.bases = [_Base(parameters[4 * i], state, dtype) for i, state in enumerate(states)]
+        factors, self.stacked = group_factors(parameters, 3, dtype, x, shared=2)
+        self.a, self.b = factors[0::2], factors[1::2]
+        self.rank = [len(a) for a in self.a]
+        self.width = int(states[GATE].shape[0]) if states[GATE] is not None else len(parameters[0])
+
+    def empty(self, *shape):
+        return torch.empty(shape, device=self.device, dtype=self.dtype)
+
+    def xa_buffer(self, rows):
+        """Storage for xa_gate and xa_up over `rows` rows: the two column halves of one
+        [rows, 2r] buffer when the stacked GEMM fills them, else two buffers."""
+        if self.stacked is not None:
+            pair = self.empty(rows, 2 * self.rank[GATE])
+            return pair, (pair[:, :self.rank[GATE]], pair[:, self.rank[GATE]:])
+        return None, (self.empty(rows, self.rank[GATE]), self.empty(rows, self.rank[UP]))
+
+    def project(self, which, x, out, xa):
+        """out = x w^T + (x a^T) b^T for one projection, xa = x a^T written."""
+        forward_linear(x, self.bases[which], self.a[which], self.b[which], out=out, xa=xa)
+
+    def gate_up(self, x, gate, up, pair, xa):
+        """gate and up of one tile. With the stacked factors their xa come from one GEMM
+        into `pair` (whose column halves are xa) and the projections read them."""
+        if self.stacked is None or not len(x):
+            self.project(GATE, x, gate, xa[GATE])
+            self.project(UP, x, up, xa[UP])
+            return
+        _low_rank(x, self.stacked, pair, transpose=True)
+        for which, out in ((GATE, gate), (UP, up)):
+            self.bases[which].forward(x, self.a[which], self.b[which], None, out, xa[which], xa_given=True)
+
+    def input_gradient(self, which, dy, dx, low, add):
+        input_gradient(dy, self.bases[which], self.a[which], self.b[which], dx, low, add=add)
+
+    def low_product(self, which, dy, low):
+        """low = dy b, when the input gradient is not needed."""
+        _low_rank(dy, self.b[which], low, transpose=False)
+
+
+def _tile_starts(rows, tile):
+    return range(0, rows, tile)
+
+
+# ----------------------------------------------------------------------------- forward
 @torch.no_grad()
 def _forward_into(output, x, dtype, tile, states, parameters, residual, *, save=False):
+    """Fill `output` (the MLP's result, plus `residual`) tile by tile. With `save`, return
+    (gate, up, xa_gate, xa_up) over all rows for the cached backward; else ()."""
     flat = x.reshape(-1, x.shape[-1]).to(dtype)
-    matrices = _bases(parameters, states, dtype)
-    cast, stack = group_factors(parameters, 3, dtype, flat, shared=2)
-    adapters = [(cast[2*i], cast[2*i+1]) for i in range(3)]
-    rows = min(tile, len(flat))
-    width = matrices[0].rows
-    workspace = torch.empty((1 if save else 2, rows, width), device=x.device, dtype=dtype)
-    low = torch.empty((rows, max(len(a) for a, _ in adapters)), device=x.device, dtype=dtype)
-    r = len(adapters[0][0])
-    # gate and up read the same rows: with a shared rank their xa come from one GEMM over
-    # [a_gate; a_up] into the two column halves of one buffer.
-    pair = None if stack is None or save else torch.empty((rows, 2 * r), device=x.device, dtype=dtype)
+    rows = len(flat)
+    mlp = _MLPProjections(parameters, states, dtype, flat)
+    span = min(tile, rows)
+    target = output.view(rows, -1)
+    xa_down = mlp.empty(span, mlp.rank[DOWN])
     if save:
-        if stack is not None:
-            both = torch.empty((len(flat), 2 * r), device=x.device, dtype=dtype)
-            held = (both[:, :r], both[:, r:])
-        else:
-            held = tuple(torch.empty((len(flat), len(a)), device=x.device, dtype=dtype) for a, _ in adapters[:2])
-    saved = (() if not save else (
-        *(torch.empty((len(flat), width), device=x.device, dtype=dtype) for _ in range(2)), *held))
-    destination = output.view_as(flat)
-    for start in range(0, len(flat), tile):
-        part = flat[start:start+tile]
-        gate, up = ((buffer[start:start+len(part)] for buffer in saved[:2]) if save
-                    else (buffer[:len(part)] for buffer in workspace))
-        xa = [low[:len(part), :len(a)] for a, _ in adapters]
+        gate_all, up_all = mlp.empty(rows, mlp.width), mlp.empty(rows, mlp.width)
+        pair_all, xa_all = mlp.xa_buffer(rows)
+        hidden_tile = mlp.empty(span, mlp.width)
+    else:
+        gate_tile, up_tile = mlp.empty(span, mlp.width), mlp.empty(span, mlp.width)
+        pair_tile, xa_tile = mlp.xa_buffer(span)
+    for start in _tile_starts(rows, tile):
+        part = flat[start:start + tile]
+        n = len(part)
         if save:
-            xa[:2] = [buffer[start:start+len(part)] for buffer in saved[2:]]
-        elif pair is not None:
-            xa[:2] = [pair[:len(part), :r], pair[:len(part), r:]]
-        _gate_up(part, matrices, adapters, gate, up, xa, stack)
-        hidden = activation(gate, up, out=workspace[0, :len(part)] if save else gate)
-        forward_linear(hidden, matrices[2], *adapters[2], out=destination[start:start+tile], xa=xa[2])
+            window = slice(start, start + n)
+            gate, up = gate_all[window], up_all[window]
+            pair = None if pair_all is None else pair_all[window]
+            xa = tuple(value[window] for value in xa_all)
+            hidden = hidden_tile[:n]
+        else:
+            gate, up = gate_tile[:n], up_tile[:n]
+            pair = None if pair_tile is None else pair_tile[:n]
+            xa = tuple(value[:n] for value in xa_tile)
+            hidden = gate   # h overwrites the tile's gate, which is not needed after it
+        mlp.gate_up(part, gate, up, pair, xa)
+        activation(gate, up, out=hidden)
+        mlp.project(DOWN, hidden, target[start:start + n], xa_down[:n])
     if residual is not None:
         output.add_(residual)
-    return saved
+    return (gate_all, up_all, *xa_all) if save else ()
 
 
-def _gate_up(part, matrices, adapters, gate, up, xa, stack):
-    """gate and up of one tile; with `stack` their xa (two column halves of one buffer)
-    come from one GEMM first."""
-    if stack is None or not len(part):
-        forward_linear(part, matrices[0], *adapters[0], out=gate, xa=xa[0])
-        forward_linear(part, matrices[1], *adapters[1], out=up, xa=xa[1])
-        return
-    r = len(adapters[0][0])
-    both = xa[0].as_strided((len(part), 2 * r), xa[0].stride())
-    _low_rank(part, stack, both, transpose=True)
-    matrices[0].forward(part, *adapters[0], None, gate, xa[0], xa_given=True)
-    matrices[1].forward(part, *adapters[1], None, up, xa[1], xa_given=True)
+# ----------------------------------------------------------------------------- backward
+def _backward(ctx, grad, x, kept, parameters):
+    dtype, tile = ctx.dtype, ctx.tile
+    flat = x.reshape(-1, x.shape[-1]).to(dtype)
+    upstream = grad.reshape_as(flat).to(dtype)
+    rows = len(flat)
+    dx = torch.empty_like(flat) if ctx.needs_input_grad[0] else None
+    mlp = _MLPProjections(parameters, ctx.states, dtype, flat)
+    # fp32 adapter gradients; zeros when there are no rows (nothing accumulates into them)
+    fresh = torch.empty_like if rows else torch.zeros_like
+    grads = [(fresh(parameters[4 * i + 1]), fresh(parameters[4 * i + 2])) for i in range(3)]
+    span = min(tile, rows)
+    # three [tile, width] buffers: (gate, up, dh) in, (d gate, d up, h) out
+    first, second, third = (mlp.empty(span, mlp.width) for _ in range(3))
+    low = mlp.empty(span, max(mlp.rank))
+    xa_down = mlp.empty(span, mlp.rank[DOWN])
+    pair_tile, xa_tile = (None, None) if kept else mlp.xa_buffer(span)
+    for start in _tile_starts(rows, tile):
+        part, dy = flat[start:start + tile], upstream[start:start + tile]
+        n = len(part)
+        window = slice(start, start + n)
+        d_gate, d_up, d_hidden = first[:n], second[:n], third[:n]
+        if kept:
+            xa = (kept[2][window], kept[3][window])
+        else:
+            xa = tuple(value[:n] for value in xa_tile)
+            mlp.gate_up(part, d_gate, d_up, None if pair_tile is None else pair_tile[:n], xa)
+        mlp.input_gradient(DOWN, dy, d_hidden, low[:n, :mlp.rank[DOWN]], False)
+        if kept:
+            # Read the kept gate/up, write d gate / d up into the tile buffers and h over dh.
+            _silu_kernel(kept[0][window], kept[1][window], d_hidden, d_gate, d_up, backward=True, reconstruct=True)
+        else:
+            activation(d_gate, d_up, d_hidden)
+        hidden = d_hidden
+        _low_rank(hidden, mlp.a[DOWN], xa_down[:n], transpose=True)
+        parameter_gradients(hidden, dy, *grads[DOWN], low[:n, :mlp.rank[DOWN]], xa_down[:n], add=start > 0)
+        for which, signal in ((GATE, d_gate), (UP, d_up)):
+            grad_low = low[:n, :mlp.rank[which]]
+            if dx is not None:
+                mlp.input_gradient(which, signal, dx[window], grad_low, which == UP)
+            else:
+                mlp.low_product(which, signal, grad_low)
+            parameter_gradients(part, signal, *grads[which], grad_low, xa[which], add=start > 0)
+    if dx is not None:
+        dx = dx.reshape_as(x).to(x.dtype)
+    return dx, [value for da, db in grads for value in (None, da, db, None)]
 
 
 class _TiledLoRAMLP(torch.autograd.Function):
-    """Saves only the input and the parameters (plus, in cache mode, gate/up and their xa);
-    the backward recomputes gate/up per tile and never builds an autograd graph."""
+    """Saves the input and the parameters, plus (cache mode) gate, up and their xa. Outside
+    cache mode the forward only registers what it saves and returns an empty output that
+    `tiled_lora_mlp` fills with `_forward_into`, so a checkpoint replay that needs no
+    output can stop before any GEMM (reference mlp_cuda.py:94-97)."""
 
     @staticmethod
     def forward(ctx, x, dtype, tile, states, residual, cache, *parameters):
-        ctx.dtype, ctx.tile, ctx.states = dtype, tile, states
-        ctx.cache = cache
-        if cache:
-            output = torch.empty(x.shape, device=x.device, dtype=dtype)
-            saved = _forward_into(output, x, dtype, tile, states, parameters, residual, save=True)
-            ctx.save_for_backward(x, *saved, *parameters)
-            return output
-        # Register the saved inputs before the wrapper fills this private output, so a
-        # checkpoint replay can stop before the GEMMs (reference mlp_cuda.py:94-97).
-        ctx.save_for_backward(x, *parameters)
-        return torch.empty(x.shape, device=x.device, dtype=dtype)
+        ctx.dtype, ctx.tile, ctx.states, ctx.cache = dtype, tile, states, cache
+        output = torch.empty(x.shape, device=x.device, dtype=dtype)
+        kept = _forward_into(output, x, dtype, tile, states, parameters, residual, save=True) if cache else ()
+        ctx.save_for_backward(x, *kept, *parameters)
+        return output
 
     @staticmethod
     def backward(ctx, grad):
-        x, *parameters = ctx.saved_tensors
-        saved = parameters[:4] if ctx.cache else ()
-        if ctx.cache:
-            parameters = parameters[4:]
+        x, *rest = ctx.saved_tensors
+        kept, parameters = (rest[:4], rest[4:]) if ctx.cache else ((), rest)
+        dx, adapter_grads = _backward(ctx, grad, x, kept, parameters)
         residual_grad = grad if ctx.needs_input_grad[4] else None
-        flat = x.reshape(-1, x.shape[-1]).to(ctx.dtype)
-        grad = grad.reshape_as(flat).to(ctx.dtype)
-        dx = torch.empty_like(flat) if ctx.needs_input_grad[0] else None
-        matrices = _bases(parameters, ctx.states, ctx.dtype)
-        cast, stack = group_factors(parameters, 3, ctx.dtype, flat, shared=2)
-        adapters = [(cast[2*i], cast[2*i+1]) for i in range(3)]
-        allocate = torch.empty_like if len(flat) else torch.zeros_like
-        gradients = [(allocate(parameters[4*i+1]), allocate(parameters[4*i+2])) for i in range(3)]
-        rows = min(ctx.tile, len(flat))
-        workspace = torch.empty((3, rows, matrices[0].rows), device=x.device, dtype=ctx.dtype)
-        if stack is not None and not ctx.cache:
-            r = len(adapters[0][0])
-            pair = torch.empty((rows, 2 * r), device=x.device, dtype=ctx.dtype)
-            low_inputs = [pair[:, :r], pair[:, r:],
-                          torch.empty((rows, len(adapters[2][0])), device=x.device, dtype=ctx.dtype)]
-        else:
-            low_inputs = [torch.empty((rows, len(a)), device=x.device, dtype=ctx.dtype) for a, _ in adapters]
-        low_grad = torch.empty((rows, max(len(a) for a, _ in adapters)), device=x.device, dtype=ctx.dtype)
-        for start in range(0, len(flat), ctx.tile):
-            part, dy = flat[start:start+ctx.tile], grad[start:start+ctx.tile]
-            gate, up, dh = (buffer[:len(part)] for buffer in workspace)
-            xa = [buffer[:len(part)] for buffer in low_inputs]
-            low = [low_grad[:len(part), :len(a)] for a, _ in adapters]
-            if ctx.cache:
-                xa[:2] = [value[start:start+len(part)] for value in saved[2:]]
-            else:
-                _gate_up(part, matrices, adapters, gate, up, xa, stack)
-            input_gradient(dy, matrices[2], *adapters[2], dh, low[2])
-            if ctx.cache:
-                # The saved gate/up stay untouched (a repeated backward reads them again):
-                # the activation backward reads them and writes d gate, d up into the tile
-                # buffers and hidden over dh, where the reference copies the tile first.
-                _silu(saved[0][start:start+len(part)], saved[1][start:start+len(part)], dh, gate, up, True, True)
-                hidden = dh
-            else:
-                # Reuse the three wide tile buffers: (gate, up, dh) -> (d gate, d up, hidden).
-                hidden = activation(gate, up, dh)
-            _low_rank(hidden, adapters[2][0], xa[2], transpose=True)
-            parameter_gradients(hidden, dy, *gradients[2], low[2], xa[2], add=start > 0)
-            for index, signal in enumerate((gate, up)):
-                if dx is not None:
-                    input_gradient(signal, matrices[index], *adapters[index], dx[start:start+ctx.tile], low[index],
-                                   add=index > 0)
-                else:
-                    _low_rank(signal, adapters[index][1], low[index], transpose=False)
-                parameter_gradients(part, signal, *gradients[index], low[index], xa[index], add=start > 0)
-        result = [value for da, db in gradients for value in (None, da, db, None)]
-        return (None if dx is None else dx.reshape_as(x).to(x.dtype), None, None, None, residual_grad, None, *result)
+        return (dx, None, None, None, residual_grad, None, *adapter_grads)
 
 
 def tiled_lora_mlp(module, x, residual=None, *, tile=None, cache=None):
-    """`module` carries gate_proj, up_proj, down_proj (Projection), tile and
-    cache_intermediates, as the reference's MLP (modeling/model.py:111-139) does."""
-    modules = (module.gate_proj, module.up_proj, module.down_proj)
-    dtype = modules[0].compute_dtype
-    if residual is not None and (residual.shape != x.shape or residual.dtype != dtype):
-        return tiled_lora_mlp(module, x, tile=tile, cache=cache)+residual
+    """The MLP of `module` (gate_proj, up_proj, down_proj, tile, cache_intermediates; the
+    reference's modeling/model.py:111-139) on x, plus `residual`."""
+    projections = (module.gate_proj, module.up_proj, module.down_proj)
+    dtype = projections[0].compute_dtype
+    if residual is not None and (residual.dtype != dtype or residual.shape != x.shape):
+        return tiled_lora_mlp(module, x, tile=tile, cache=cache) + residual
     parameters, states = [], []
-    for projection in modules:
+    for projection in projections:
         values, state = projection_parameters(projection)
-        parameters.extend(values)
+        parameters += values
         states.append(state)
-    tile = (module.tile if tile is None else tile) or max(1, x.numel()//x.shape[-1])
-    cache = (module.cache_intermediates if cache is None else cache) and torch.is_grad_enabled()
+    rows = x.numel() // x.shape[-1]
+    tile = (tile if tile is not None else module.tile) or max(1, rows)
+    cache = bool(module.cache_intermediates if cache is None else cache) and torch.is_grad_enabled()
     output = _TiledLoRAMLP.apply(x, dtype, tile, tuple(states), residual, cache, *parameters)
     if not cache:
         _forward_into(output, x, dtype, tile, states, parameters, residual)

@@ -165,16 +165,21 @@ class Decoder(nn.Module):
                 retained += cost
         return retained
 
-    def hidden(self, ids, records, *, mlp_cache_bytes=0):
+    def hidden(self, ids, records, *, mlp_cache_bytes=0, projection_bytes=0):
+        """Final hidden states. `projection_bytes` is the per-group projection budget
+        (kernels.linear.projection_budget): 0 keeps the reference's 4096-row tiles and
+        saved tensors, a budget that covers a group's rows keeps its forward xa."""
+        from ..kernels.linear import projection_budget
         positions = record_positions(records, ids.device)
         cosine, sine = rotary_values(positions, self.config, torch.bfloat16)
         x = self.embed_tokens(ids)
         self.plan_mlp_cache(ids.numel() if ids.is_cuda else 0, mlp_cache_bytes)
-        for layer in self.layers:
-            x = layer(x, cosine, sine, records)
+        with projection_budget(projection_bytes):
+            for layer in self.layers:
+                x = layer(x, cosine, sine, records)
         return self.norm(x)
 
-    def loss(self, ids, targets, weights, records, *, token_budget=128, mlp_cache_bytes=0):
+    def loss(self, ids, targets, weights, records, *, token_budget=128, mlp_cache_bytes=0, projection_bytes=0):
         from ..kernels.loss import projection_loss
-        return projection_loss(self.hidden(ids, records, mlp_cache_bytes=mlp_cache_bytes), self.lm_head.weight,
-                               targets, weights, token_budget=token_budget)
+        hidden = self.hidden(ids, records, mlp_cache_bytes=mlp_cache_bytes, projection_bytes=projection_bytes)
+        return projection_loss(hidden, self.lm_head.weight, targets, weights, token_budget=token_budget)

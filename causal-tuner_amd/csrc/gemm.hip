@@ -31,7 +31,6 @@
 // Workgroup ids are remapped so each of the 8 XCDs walks a contiguous, M-grouped range of
 // output tiles: the workgroups that share an L2 also share A and B panels.
 
-#include <cstdio>
 #include <cstdlib>
 
 #include "gemm_common.hpp"
@@ -1208,17 +1207,6 @@ hipError_t run(Problem &pr, hipStream_t s) {
 // Tile and split count for a reduction-heavy GEMM with a small output (dA, dB): enough
 // workgroups for about one per CU, at least 8 k-tiles per split, at most 32 splits.
 void choose_reduction(int64_t m, int64_t n, int64_t kred, int *tile, int *splits) {
-#ifdef CT_TUNING
-    if (const char *env = getenv("CT_RED")) {
-        int t = 1, sp = 4;
-        if (sscanf(env, "%d,%d", &t, &sp) == 2) {
-            *tile = t;
-            const int64_t ktiles = cdiv(kred, kBK);
-            *splits = (int)(sp < 1 ? 1 : (sp > ktiles ? ktiles : sp));
-            return;
-        }
-    }
-#endif
     *tile = (m >= 128 && n >= 128) ? TILE_128 : TILE_64;
     const int64_t e = kTileEdge[*tile];
     const int64_t tiles_out = cdiv(m, e) * cdiv(n, e);
@@ -1371,15 +1359,6 @@ bool lowrank_split(int64_t m, int64_t n, int64_t k, int *tile, int *splits) {
     int64_t s = 512 / tiles;
     *tile = TILE_128;
     *splits = (int)(s < 2 ? 2 : (s > 4 ? 4 : s));
-#ifdef CT_TUNING
-    if (const char *env = getenv("CT_LOWRANK")) {
-        int t = 0, sp = 0;
-        if (sscanf(env, "%d,%d", &t, &sp) == 2) {
-            *tile = t;
-            *splits = sp;
-        }
-    }
-#endif
     return true;
 }
 }  // namespace
@@ -1422,14 +1401,6 @@ extern "C" int ct_gemm(const void *a, int64_t lda, int32_t trans_a, const void *
     pr.ws = workspace;
     pr.ws_bytes = workspace ? workspace_bytes : 0;
     pr.vec = vec_ok(pr);
-#ifdef CT_TUNING
-    if (getenv("CT_GEMM_RED") && !bias && workspace) {
-        int status = 0;
-        const hipError_t e = run_reduction(pr, c, ldc, beta, workspace, workspace_bytes, stream, &status);
-        return status ? status : to_status(e);
-    }
-    if (const char *env = getenv("CT_TILE")) pr.tile = atoi(env);
-#endif
     int tile, splits;
     if (!bias && c_dtype == CT_BF16 && !trans_a && lowrank_split(m, n, k, &tile, &splits) && workspace &&
         workspace_bytes >= (int64_t)splits * m * n * 4) {
@@ -1689,18 +1660,6 @@ ParamPlan param_plan(int64_t m, int64_t n, int64_t k, int64_t r) {
     if (s > cap) s = cap;
     if (s > 8) s = 8;
     pl.splits = (int)(s < 1 ? 1 : s);
-#ifdef CT_TUNING
-    if (const char *env = getenv("CT_PARAM")) {
-        int t = 0, sp = 1;
-        if (sscanf(env, "%d,%d", &t, &sp) == 2) {
-            pl.tile = t;
-            const int64_t e2 = kTileEdge[t];
-            pl.gt = (int)cdiv(k, e2);
-            pl.width = pl.gt * e2 + n;
-            pl.splits = sp;
-        }
-    }
-#endif
     return pl;
 }
 int64_t param_workspace(const ParamPlan &pl, int64_t r) { return (int64_t)pl.splits * r * pl.width * 4; }

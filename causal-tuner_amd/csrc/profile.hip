@@ -59,12 +59,28 @@ extern "C" int ct_profile_begin(int32_t families, int32_t capacity) {
     if (families <= 0 || capacity <= 0) return -CT_EINVAL_SHAPE;
     std::lock_guard<std::mutex> lock(g_mutex);
     if (g_families.load() != 0) return -CT_EINVAL_POINTER;  // already profiling
-    g_slots.assign((size_t)capacity, Slot{});
-    for (auto &s : g_slots) {
-        hipError_t e = hipEventCreate(&s.start);
-        if (e == hipSuccess) e = hipEventCreate(&s.stop);
-        if (e != hipSuccess) return (int)e;
+    // Build the pool aside and publish it only when every event exists; on a failure the
+    // events created so far are destroyed and the profiler stays closed.
+    std::vector<Slot> slots((size_t)capacity, Slot{});
+    size_t created = 0;
+    hipError_t e = hipSuccess;
+    for (; created < slots.size(); ++created) {
+        e = hipEventCreate(&slots[created].start);
+        if (e != hipSuccess) break;
+        e = hipEventCreate(&slots[created].stop);
+        if (e != hipSuccess) {
+            hipEventDestroy(slots[created].start);
+            break;
+        }
     }
+    if (e != hipSuccess) {
+        for (size_t i = 0; i < created; ++i) {
+            hipEventDestroy(slots[i].start);
+            hipEventDestroy(slots[i].stop);
+        }
+        return (int)e;
+    }
+    g_slots.swap(slots);
     g_used = 0;
     g_families.store(families);
     return 0;

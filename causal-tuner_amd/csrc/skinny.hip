@@ -635,15 +635,6 @@ SkShape sk_shape(const GemmParams &p, bool columns, int64_t ws_floats) {
     // Whole rounds of resident workgroups: splits * groups a multiple of the target when
     // the columns alone do not fill the GPU.
     int64_t splits = groups >= target ? 1 : cdiv(target, groups);
-#ifdef CT_TUNING
-    if (const char *env = getenv(columns ? "CT_SKT" : "CT_SKR")) {
-        int nb = 0, sp = 0;
-        if (sscanf(env, "%d,%d", &nb, &sp) == 2) {
-            if (!columns && nb > 0) sh.nb = nb;
-            if (sp > 0) splits = sp;
-        }
-    }
-#endif
     const int64_t cap = steps / min_steps > 1 ? steps / min_steps : 1;
     if (splits > cap) splits = cap;
     if (splits > 64) splits = 64;
@@ -737,7 +728,9 @@ int64_t skinny_workspace_bytes(const GemmParams &p, const int src_b[2]) {
 hipError_t skinny_run(GemmParams p, const int src_b[2], void *ws, int64_t ws_bytes, hipStream_t stream) {
     const int b0 = src_b[0], b1 = p.nseg > 1 ? src_b[1] : src_b[0];
     const bool columns = column_src(b0);
-    const SkShape sh = sk_shape(p, columns, ws ? ws_bytes / 4 : 0);
+    // The partials are written with 16-byte stores: a misaligned workspace counts as none
+    // (no split), as the many-row paths treat it.
+    const SkShape sh = sk_shape(p, columns, (ws && aligned16(ws)) ? ws_bytes / 4 : 0);
     p.split_ws = static_cast<float *>(ws);
     p.split_stride = p.m * p.n;
     hipError_t e = hipErrorNotSupported;

@@ -77,9 +77,12 @@ __device__ __forceinline__ void ce_store_vec(void *p, int64_t i, const float (&v
     *reinterpret_cast<uint4 *>(static_cast<char *>(p) + i * (DT == CT_F32 ? 4 : 2)) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// (m, s) represents s * exp(m); combining keeps the larger maximum.
+// (m, s) represents s * exp(m); combining keeps the larger maximum. A NaN on either side
+// makes the pair NaN, so a NaN logit gives a NaN loss as sum(exp(values - max)) does.
 __device__ __forceinline__ void combine(float &m, float &s, float m2, float s2) {
-    if (m2 > m) {
+    if (__builtin_isnan(m2) || __builtin_isnan(s2)) {
+        m = s = __builtin_nanf("");
+    } else if (m2 > m) {
         s = s * __expf(m - m2) + s2;
         m = m2;
     } else if (m2 > -INFINITY) {

@@ -128,7 +128,8 @@ int ct_nf4_quantize(const void *w, int32_t w_dtype, int64_t n, int32_t blocksize
  * reduction may be split across workgroups, the fp32 partials going to the caller's
  * workspace and summed in a fixed order (results do not depend on timing). The *_workspace
  * query gives the size that allows the preferred split; a null or smaller workspace is
- * valid and only splits less (no split at all without one).
+ * valid and only splits less (no split at all without one). The partials are written with
+ * 16-byte stores, so a workspace that is not 16-byte aligned is treated as absent.
  */
 int64_t ct_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t trans_a, int32_t trans_b, int32_t c_dtype);
 int ct_gemm(const void *a, int64_t lda, int32_t trans_a,

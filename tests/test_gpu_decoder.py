@@ -11,6 +11,7 @@ import math
 import pytest
 import torch
 import torch.nn.functional as F
+from torch.utils.checkpoint import checkpoint
 
 pytestmark = pytest.mark.gpu
 
@@ -28,26 +29,30 @@ def _tiny():
     return model
 
 
-def _host_loss(model, ids, targets, weights, records):
-    """Float32 host restatement; returns (loss, {parameter name: leaf clone})."""
+def _host_loss(model, ids, targets, weights, records, device="cpu", dtype=torch.float32):
+    """The model restated in plain torch on `device` (the host by default) with activations
+    in `dtype` (float32 by default; the LoRA leaves are float32 masters cast per product);
+    returns (loss, {parameter name: leaf clone})."""
     c = model.config
     leaves = {}
 
     def leaf(name, p):
-        leaves[name] = p.detach().float().cpu().requires_grad_(True)
-        return leaves[name]
+        leaves[name] = p.detach().float().to(device).requires_grad_(True)
+        return leaves[name].to(dtype)
 
     modules = dict(model.named_modules())
 
     def project(name, x):
         p = modules[name]
-        out = x @ p.base_weight().float().cpu().T
+        out = x @ p.base_weight().to(device, dtype).T
         if p.bias is not None:
-            out = out + p.bias.float().cpu()
+            out = out + p.bias.to(device, dtype)
         return out + (x @ leaf(name + ".lora_A", p.lora_A).T) @ leaf(name + ".lora_B", p.lora_B).T
 
     def norm(module, x):
-        return x * torch.rsqrt(x.square().mean(-1, keepdim=True) + c.rms_norm_eps) * module.weight.float().cpu()
+        wide = x.float()
+        normed = (wide * torch.rsqrt(wide.square().mean(-1, keepdim=True) + c.rms_norm_eps)).to(dtype)
+        return normed * module.weight.to(device, dtype)
 
     def rope(x, cos, sin):
         half = cos.shape[-1]
@@ -57,32 +62,38 @@ def _host_loss(model, ids, targets, weights, records):
         turned = torch.stack((a * cs - b * sn, b * cs + a * sn), -1).flatten(-2)
         return torch.cat((turned, x[..., 2 * half:]), -1)
 
-    positions = torch.cat([torch.arange(e - s) for s, e in records]).float()
-    channel = torch.arange(0, c.rotary_dim, 2, dtype=torch.float32)
+    def attend(q, k, v):
+        parts = []
+        for s, e in records:
+            # [heads, q, d] @ [d, k] with the single key head shared: plain contiguous products
+            query = q[s:e].transpose(0, 1)
+            scores = (query @ k[s:e, 0].T.contiguous()).float() / math.sqrt(c.head_dim)
+            mask = torch.ones(e - s, e - s, dtype=torch.bool, device=device).tril()
+            probs = scores.masked_fill(~mask, float("-inf")).softmax(-1).to(dtype)
+            parts.append((probs @ v[s:e, 0]).transpose(0, 1))
+        return torch.cat(parts).flatten(-2)
+
+    positions = torch.cat([torch.arange(e - s) for s, e in records]).float().to(device)
+    channel = torch.arange(0, c.rotary_dim, 2, dtype=torch.float32, device=device)
     angle = positions[:, None] * (1.0 / (c.rope_theta ** (channel / c.rotary_dim)))
-    cos, sin = angle.cos(), angle.sin()
-    x = model.embed_tokens.weight.detach().float().cpu()[ids.cpu()]
+    cos, sin = angle.cos().to(dtype), angle.sin().to(dtype)
+    x = model.embed_tokens.weight.detach().to(device, dtype)[ids.to(device)]
     for index, layer in enumerate(model.layers):
         pre = f"layers.{index}."
         h = norm(layer.input_layernorm, x)
         q = rope(project(pre + "self_attn.q_proj", h).unflatten(-1, (c.num_attention_heads, c.head_dim)), cos, sin)
         k = rope(project(pre + "self_attn.k_proj", h).unflatten(-1, (1, c.head_dim)), cos, sin)
         v = project(pre + "self_attn.v_proj", h).unflatten(-1, (1, c.head_dim))
-        parts = []
-        for s, e in records:
-            scores = torch.einsum("qhd,khd->hqk", q[s:e], k[s:e].expand(-1, c.num_attention_heads, -1))
-            scores = scores / math.sqrt(c.head_dim)
-            mask = torch.ones(e - s, e - s, dtype=torch.bool).tril()
-            probs = scores.masked_fill(~mask, float("-inf")).softmax(-1)
-            parts.append(torch.einsum("hqk,khd->qhd", probs, v[s:e].expand(-1, c.num_attention_heads, -1)))
-        y = torch.cat(parts).flatten(-2)
+        # recomputed in the backward, so the [heads, len, len] scores of every layer are
+        # not all held at once
+        y = checkpoint(attend, q, k, v, use_reentrant=False)
         x = x + project(pre + "self_attn.o_proj", y)
         h = norm(layer.post_attention_layernorm, x)
         g = project(pre + "mlp.gate_proj", h)
         u = project(pre + "mlp.up_proj", h)
         x = x + project(pre + "mlp.down_proj", F.silu(g) * u)
-    logits = norm(model.norm, x) @ model.lm_head.weight.detach().float().cpu().T
-    loss = (F.cross_entropy(logits, targets.cpu(), reduction="none") * weights.cpu()).sum()
+    logits = (norm(model.norm, x) @ model.lm_head.weight.to(device, dtype).T).float()
+    loss = (F.cross_entropy(logits, targets.to(device), reduction="none") * weights.to(device)).sum()
     return loss, leaves
 
 

@@ -337,27 +337,60 @@ def test_shared_group_with_bf16_adapters():
 
 @pytest.mark.parametrize("count", [1, 3])
 def test_backward_reads_the_forward_xa(monkeypatch, count):
-    """With one tile over all rows the group keeps each projection's forward xa = x a^T and
-    the backward runs no rank-r GEMM on x again; its gradients equal those of the tiled
-    backward, which recomputes xa per tile as the reference does (linear.py:124-125)."""
+    """Under a projection budget that covers the input, the group runs one tile, keeps each
+    projection's forward xa = x a^T and the backward runs no rank-r GEMM on x again; its
+    gradients equal those of the tiled backward, which recomputes xa per tile as the
+    reference does (linear.py:124-125)."""
     from causal_tuner.kernels import linear
     modules = [_projection(256, n, 32, seed=7 + i) for i, n in enumerate((256, 64, 64)[:count])]
     x = torch.randn(512, 256, device="cuda", dtype=torch.bfloat16, requires_grad=True)
-    outputs = linear.project_group(modules, x)
+    with linear.projection_budget(1 << 30):
+        outputs = linear.project_group(modules, x)
     signals = [torch.randn_like(out) for out in outputs]
     params = [x, *(p for m in modules for p in (m.lora_A, m.lora_B))]
     calls = []
-    for name in ("_shared_xa", "_low_rank"):
-        original = getattr(linear, name)
-        monkeypatch.setattr(linear, name, lambda *args, _f=original, _n=name, **kw: (
-            calls.append((_n, kw.get("transpose", True))), _f(*args, **kw))[1])
+    original = linear._low_rank
+    monkeypatch.setattr(linear, "_low_rank", lambda *args, **kw: (
+        calls.append(kw.get("transpose", True)), original(*args, **kw))[1])
     kept = torch.autograd.grad(outputs, params, signals)
     monkeypatch.undo()
     # no x [a_1; ...]^T and no x a^T in the backward (low = dy b would be transpose=False)
-    assert not [call for call in calls if call[1]], calls
+    assert not [call for call in calls if call], calls
     tiled = linear.project_group(modules, x, 128)
     recomputed = torch.autograd.grad(tiled, params, signals)
     for out, again in zip(outputs, tiled):
         assert torch.equal(out, again) or ((out.float() - again.float()).norm() / again.float().norm()).item() < 1e-2
     for a, b in zip(kept, recomputed):
         assert ((a.float() - b.float()).norm() / b.float().norm()).item() < 1e-2
+
+
+def test_default_group_saves_only_inputs_and_parameters(monkeypatch):
+    """Without a budget a group keeps the reference's contract (linear.py:62-63,
+    test_fast_training.py:143-158): only the input and the parameters are saved, and the
+    backward's rank-r products see at most 4096 rows at a time."""
+    from causal_tuner.kernels import linear
+    modules = [_projection(64, n, 8, seed=11 + i) for i, n in enumerate((64, 32, 32))]
+    x = torch.randn(4099, 64, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    saved = []
+
+    def pack(tensor):
+        saved.append(tensor)
+        return tensor
+    with torch.autograd.graph.saved_tensors_hooks(pack, lambda tensor: tensor):
+        outputs = linear.project_group(modules, x)
+    allowed = {x.data_ptr(), *(p.data_ptr() for m in modules for p in m.parameters())}
+    allowed |= {m.quantized.weight.data_ptr() for m in modules if m.quantized is not None}
+    assert saved and all(t is None or t.data_ptr() in allowed for t in saved)
+    rows = []
+    original = linear._low_rank
+    monkeypatch.setattr(linear, "_low_rank", lambda x_, *args, **kw: (rows.append(len(x_)), original(x_, *args, **kw))[1])
+    grads = torch.autograd.grad(outputs, [x, *(p for m in modules for p in (m.lora_A, m.lora_B))],
+                                [torch.randn_like(o) for o in outputs])
+    monkeypatch.undo()
+    assert rows and max(rows) <= 4096
+    with linear.projection_budget(1 << 30):
+        again = linear.project_group(modules, x)
+    whole = torch.autograd.grad(again, [x, *(p for m in modules for p in (m.lora_A, m.lora_B))],
+                                [torch.randn_like(o) for o in outputs])
+    for a, b in zip(grads, whole):
+        assert a.shape == b.shape and bool(torch.isfinite(a).all())
