@@ -4,7 +4,7 @@ Every kernel source under csrc/ is compiled by hipcc for gfx950 only and linked 
 shared library that exports the C ABI of include/causal_tuner_hip.h. The library is loaded
 with ctypes after torch, so it binds to the HIP runtime torch already mapped (same soname).
 
-    python causal-tuner_amd/build.py [--jobs N]
+    python causal-tuner_amd/build.py [--jobs N] [--incremental]
 """
 
 import argparse
@@ -49,13 +49,27 @@ def _compile(src):
     return obj
 
 
-def build(jobs=None, verbose=True):
+def _stale(src):
+    """True when src's object is missing or older than src or any header it may include."""
+    obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
+    if not os.path.exists(obj):
+        return True
+    headers = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hpp", ".h"))]
+    headers.append(os.path.join(ROOT, "include", "causal_tuner_hip.h"))
+    return os.path.getmtime(obj) < max(os.path.getmtime(p) for p in [src, *headers])
+
+
+def build(jobs=None, verbose=True, incremental=False):
+    """Compile every source (or, with `incremental`, only those whose object is stale) and
+    link the library."""
     os.makedirs(OBJ_DIR, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
     srcs = sources()
-    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2) // 2))
+    todo = [src for src in srcs if _stale(src)] if incremental else srcs
+    jobs = jobs or min(max(len(todo), 1), max(1, (os.cpu_count() or 2) // 2))
     with ThreadPoolExecutor(jobs) as pool:
-        objs = list(pool.map(_compile, srcs))
+        list(pool.map(_compile, todo))
+    objs = [os.path.join(OBJ_DIR, os.path.basename(src) + ".o") for src in srcs]
     out = library_path()
     tmp = out + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
@@ -71,5 +85,7 @@ def build(jobs=None, verbose=True):
 if __name__ == "__main__":
     parser = argparse.ArgumentParser()
     parser.add_argument("--jobs", type=int, default=None)
-    build(parser.parse_args().jobs)
+    parser.add_argument("--incremental", action="store_true", help="recompile only stale objects")
+    args = parser.parse_args()
+    build(args.jobs, incremental=args.incremental)
     sys.exit(0)

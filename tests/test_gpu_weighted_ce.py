@@ -94,3 +94,23 @@ def test_weighted_ce_row_pitch_and_split_edges(dtype, pad):
     torch.testing.assert_close(logits.double(), want_grad.to(dtype).double(), rtol=tol, atol=1e-6)
     if pad:
         assert torch.equal(storage[:, vocab:], before[:, vocab:])
+
+
+@pytest.mark.parametrize("column", [3, 5000])
+def test_nan_logit_gives_nan_loss(column):
+    """A NaN logit in a non-target column makes that row's loss NaN, as sum(exp(values -
+    max)) does in the reference's kernel, so a diverging step does not report a finite
+    loss; the other rows are unaffected."""
+    from causal_tuner.kernels.loss_cuda import weighted_ce
+    logits = torch.randn(3, 8192, device="cuda").to(torch.bfloat16)
+    logits[1, column] = float("nan")
+    targets = torch.tensor([7, 7, 7], device="cuda")
+    weights = torch.ones(3, device="cuda")
+    loss = weighted_ce(logits.clone(), targets, weights, gradient=False)
+    assert torch.isnan(loss[1])
+    assert bool(torch.isfinite(loss[[0, 2]]).all())
+    want = torch.nn.functional.cross_entropy(logits[[0, 2]].float(), targets[[0, 2]], reduction="none")
+    torch.testing.assert_close(loss[[0, 2]], want, rtol=2e-6, atol=1e-5)
+    grad = logits.clone()
+    weighted_ce(grad, targets, weights, gradient=True)
+    assert bool(torch.isnan(grad[1].float()).all()) and bool(torch.isfinite(grad[[0, 2]].float()).all())
