@@ -17,6 +17,7 @@ DEFAULT_LIBRARY = os.path.normpath(os.path.join(_HERE, "..", "..", "lib", "libca
 
 CT_F32, CT_F16, CT_BF16 = 0, 1, 2
 CT_CAST_MAX = 16  # tensors per ct_cast_f32_bf16 call (include/causal_tuner_hip.h)
+CT_STATIC_SCRATCH_BYTES = 64 << 20  # scratch of ct_forward_linear_static per GPU
 CT_PROF_FWD_GEMM, CT_PROF_DX_GEMM, CT_PROF_DEQUANT, CT_PROF_PARAM, CT_PROF_LOWRANK = 1, 2, 4, 8, 16
 DTYPE_CODES = {torch.float32: CT_F32, torch.float16: CT_F16, torch.bfloat16: CT_BF16}
 
@@ -46,6 +47,8 @@ _SIGNATURES = {
     "ct_forward_linear_workspace": (_I64, [_I64, _I64, _I64, _I64, _I32]),
     "ct_forward_linear": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _P, _I64, _P,
                                          _I64, _I32, _I64, _I64, _I64, _I64, _P, _I64, _P]),
+    "ct_forward_linear_static": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _P, _I64,
+                                                _P, _I64, _I32, _I64, _I64, _I64, _I64, _P]),
     "ct_input_gradient_workspace": (_I64, [_I64, _I64, _I64, _I64, _I32]),
     "ct_input_gradient": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _I64, _P,
                                          _I64, _I64, _I64, _I64, _I32, _P, _I64, _P]),
@@ -79,7 +82,7 @@ EXPORTED = tuple(_SIGNATURES)
 _library = None
 
 
-ABI_VERSION = 6   # ct_abi_version() of the library these signatures describe
+ABI_VERSION = 7   # ct_abi_version() of the library these signatures describe
 
 
 def library_path():

@@ -249,6 +249,27 @@ int ct_forward_linear(const void *x, int64_t ldx,
                       void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
+ * ct_forward_linear without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference, whose operators allocate their workspaces
+ * with torch (kernels/linear.py:67,74). Same arguments, results and row regimes as
+ * ct_forward_linear, which it calls with the library's static device scratch array of
+ * CT_STATIC_SCRATCH_BYTES per GPU (held from the library's load on that GPU until the process
+ * ends) in place of the workspace. A problem whose ct_forward_linear_workspace exceeds
+ * CT_STATIC_SCRATCH_BYTES returns -CT_EINVAL_WORKSPACE before anything is enqueued: 64 MiB
+ * covers every few-row problem and the many-row ones whose decoded weight fits (up to
+ * about 32 M weight elements). It calls no allocator. Every call on one GPU uses that GPU's
+ * one array: calls that overlap on a GPU (two streams or threads) race and must be ordered
+ * by the caller.
+ */
+#define CT_STATIC_SCRATCH_BYTES (64LL << 20)
+int ct_forward_linear_static(const void *x, int64_t ldx,
+                             const void *w_dense, const ct_nf4_weight *w_nf4,
+                             const void *a, const void *b, const void *bias,
+                             void *out, int64_t ldo, void *xa, int64_t ldxa, int32_t xa_given,
+                             int64_t m, int64_t n, int64_t k, int64_t r, hipStream_t stream);
+
+/*
  * Replaces input_gradient (kernels/linear.py:36-39):
  *   low = bf16(dy b)                                 [m, r]   (written)
  *   dx  = bf16(dy w + low a (+ dx if add))           [m, k]
