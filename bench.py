@@ -216,9 +216,22 @@ def projection_measure(device, shapes, rows_list, iters=20, rank=R):
     return results
 
 
-def cpu_baseline(budget_s=12.0):
+def _timed(fn, budget_s, max_reps=50):
+    """(reps, seconds) of fn() repeated for about budget_s after one untimed call."""
+    fn()
+    reps, start = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= budget_s or reps >= max_reps:
+            return reps, elapsed
+
+
+def cpu_baseline(budget_s=10.0):
     """The reference's torch-op sequence (oracle/lora.py) on the host CPU, bf16, for the
-    seven C3 projections over a bounded token sample."""
+    seven C3 projections over a bounded token sample, on every core of this process's
+    affinity set."""
     from oracle import lora as olora
     tokens = 1024
     threads = len(os.sched_getaffinity(0))
@@ -237,18 +250,74 @@ def cpu_baseline(budget_s=12.0):
         for w, a, b, x, dy, bias in layers:
             olora.reference_forward(x, w, a, b, bias)
             olora.reference_backward(x, w, a, b, dy)
-    run()
-    reps, start = 0, time.perf_counter()
-    while True:
-        run()
-        reps += 1
-        elapsed = time.perf_counter() - start
-        if elapsed >= budget_s or reps >= 50:
-            break
+    reps, elapsed = _timed(run, budget_s)
     flops = step_flops(tokens) * reps
     return {"value": round(flops / elapsed / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"reference torch-op sequence (oracle/lora.py), bf16 on CPU, seven C3 projections "
                       f"fwd+bwd at {tokens} of {T} tokens, {reps} reps in {elapsed:.1f} s"}
+
+
+def cpu_baselines_more(budget_s=4.0):
+    """The other CPU baselines: C1 (one 512-token 1024 -> 1024 projection, rank 16, fwd+bwd
+    through the reference's op sequence) on every affinity core and on 2 threads (the
+    reference's test harness, tests/conftest.py:8), and C2 (the [8192, 8192] NF4 decode)
+    through the plain-C restatement (oracle/nf4_dequant.c, OpenMP) on every core and on one."""
+    import ctypes
+    import numpy as np
+    from oracle import lora as olora
+    from oracle import nf4 as onf4
+    cores = len(os.sched_getaffinity(0))
+    results = {}
+    g = torch.Generator().manual_seed(4)
+    m, k, n, r = 512, 1024, 1024, 16
+    w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16)
+    a = (torch.rand(r, k, generator=g) * 2 - 1) * (6 / k) ** 0.5
+    b = torch.randn(n, r, generator=g) * 0.01
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    dy = torch.randn(m, n, generator=g).to(torch.bfloat16)
+
+    def c1():
+        olora.reference_forward(x, w, a, b)
+        olora.reference_backward(x, w, a, b, dy)
+    for threads in (cores, 2):
+        torch.set_num_threads(threads)
+        reps, elapsed = _timed(c1, budget_s, max_reps=5000)
+        results[f"C1_{threads}t"] = {
+            "value": round(projection_flops(m, k, n, r) * reps / elapsed / 1e9, 2), "unit": "GFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": f"C1 fwd+bwd (512 x 1024 -> 1024, rank 16), reference op sequence in bf16, {reps} reps "
+                      f"in {elapsed:.1f} s"}
+    torch.set_num_threads(cores)
+    lib = ctypes.CDLL(os.path.join(ROOT, "oracle", "lib", "libnf4_oracle.so"))
+    rows, cols = 8192, 8192
+    count = rows * cols
+    nb, rng = count // 64, np.random.default_rng(4)
+    packed = rng.integers(0, 256, count // 2, dtype=np.uint8)
+    qabsmax = rng.integers(0, 256, nb, dtype=np.uint8)
+    code = np.asarray(onf4.NF4_CODE, dtype=np.float32)
+    code2 = np.asarray(onf4.dynamic_map(), dtype=np.float32)
+    absmax2 = rng.random(-(-nb // 256), dtype=np.float32) * 0.1
+    out = np.empty(count, dtype=np.uint16)
+
+    def ptr(v):
+        return v.ctypes.data_as(ctypes.c_void_p)
+    lib.ct_oracle_nf4_dequant_bf16.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_float, ctypes.c_int64,
+                                                                        ctypes.c_int64, ctypes.c_int64,
+                                                                        ctypes.c_void_p]
+    nbytes = count // 2 + nb + 4 * (-(-nb // 256)) + 64 + 1024 + 4 + 2 * count
+
+    def c2():
+        lib.ct_oracle_nf4_dequant_bf16(ptr(packed), ptr(qabsmax), ptr(code), ptr(code2), ptr(absmax2), 0.01,
+                                       count, 64, 256, ptr(out))
+    for threads in (cores, 1):
+        lib.ct_oracle_set_threads(threads)
+        reps, elapsed = _timed(c2, budget_s, max_reps=2000)
+        results[f"C2_{threads}t"] = {
+            "value": round(nbytes * reps / elapsed / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "kind": "port", "sample": f"C2 [8192, 8192] NF4 decode to bf16 (synthetic packed bytes and scale "
+                                      f"codes), plain-C oracle, {reps} reps in {elapsed:.1f} s"}
+    lib.ct_oracle_set_threads(cores)
+    return results
 
 
 FAMILIES = {
@@ -572,6 +641,8 @@ def main():
         log(f"  {c4['tokens_per_s']} tokens/s, {c4['ms_per_step']} ms per step")
     cpu = None if args.no_cpu else cpu_baseline()
     log(f"cpu baseline: {cpu}")
+    cpu_more = None if args.no_cpu else cpu_baselines_more()
+    log(f"more cpu baselines: {cpu_more}")
 
     line = {
         "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -585,6 +656,7 @@ def main():
                    "flops_per_step": step_flops()},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_baselines": cpu_more,
         "kernels": families,
         "dequant": {"workload": "C2: standalone NF4 dequant to bf16", "bound": "hbm", "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "results": dequant},

@@ -36,6 +36,16 @@ void ct_oracle_nf4_dequant_bf16(const uint8_t *packed, const uint8_t *qabsmax, c
     }
 }
 
+/* Sets the OpenMP team size of the decode (the bench's CPU baseline times several). */
+void ct_oracle_set_threads(int threads) {
+#ifdef _OPENMP
+    extern void omp_set_num_threads(int);
+    omp_set_num_threads(threads);
+#else
+    (void)threads;
+#endif
+}
+
 int ct_oracle_threads(void) {
     int t = 1;
 #pragma omp parallel
