@@ -184,8 +184,8 @@ def projection_measure(device, shapes, rows_list, iters=20, rank=R):
     """One NF4-LoRA projection fwd+bwd through project_group + autograd (the reference's
     operator path), per shape and row count: average ms over `iters` steps (HIP events),
     algorithmic TFLOP/s and GB/s, and the fraction of the bound that applies (HBM for
-    few rows, bf16 MFMA for many)."""
-    from causal_tuner.kernels.linear import project_group
+    few rows, bf16 MFMA for many). Under the C3 step's projection budget, as there."""
+    from causal_tuner.kernels.linear import project_group, projection_budget
     from causal_tuner.modeling.lora import Projection
     results = {}
     for k, n in shapes:
@@ -199,7 +199,8 @@ def projection_measure(device, shapes, rows_list, iters=20, rank=R):
             dy = torch.randn(m, n, device=device, generator=g).to(torch.bfloat16)
 
             def step():
-                out, = project_group((module,), x)
+                with projection_budget(PROJECTION_BUDGET):
+                    out, = project_group((module,), x)
                 torch.autograd.grad(out, (x, module.lora_A, module.lora_B), dy)
             ms = time_events(step, iters)
             flops, nbytes = projection_flops(m, k, n, rank), skinny_bytes(m, k, n, rank)

@@ -60,6 +60,7 @@ _SIGNATURES = {
     "ct_rope": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P]),
     "ct_nf4_quantize_workspace": (_I64, [_I64, _I32, _I32]),
     "ct_nf4_quantize": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _P]),
+    "ct_quantize_blockwise": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _P]),
     "ct_rms_forward": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _P, _I64, _I64, ctypes.c_float, _P]),
     "ct_rms_backward_workspace": (_I64, [_I64, _I64, _I32]),
     "ct_rms_backward": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _P, _P, _P, _I64, _I64, _I32, _P, _I64, _P]),
@@ -82,7 +83,7 @@ EXPORTED = tuple(_SIGNATURES)
 _library = None
 
 
-ABI_VERSION = 7   # ct_abi_version() of the library these signatures describe
+ABI_VERSION = 8   # ct_abi_version() of the library these signatures describe
 
 
 def library_path():

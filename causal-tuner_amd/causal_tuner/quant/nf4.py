@@ -162,28 +162,27 @@ def _quantize_nf4_device(weight, blocksize, compress_statistics):
     midpoints = nf4_thresholds(device)
     nested = bool(compress_statistics)
     lib = _native.library()
-    if nested:
+    # First level (NF4 codes and fp32 block absmax); with double quantization the absmax
+    # then goes through bitsandbytes' second level: offset = absmax.mean() (torch's fp32
+    # mean, as quantize_4bit computes it) and absmax - offset quantized in blocks of 256.
+    first = torch.empty(nb, dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        stream = _native.stream_of(flat)
+        status = lib.ct_nf4_quantize(
+            _native.ptr(flat), _native.dtype_code(flat.dtype), n, blocksize, 0, _native.ptr(midpoints), None,
+            _native.ptr(packed), _native.ptr(first), None, None, None, 0, stream)
+        _native.check(status, "ct_nf4_quantize")
+        if not nested:
+            return packed, QuantState(first, source.shape, code, blocksize, "nf4", source.dtype)
+        offset = first.mean()
         code2 = dynamic_map().to(device)
         absmax = torch.empty(nb, dtype=torch.uint8, device=device)
         absmax2 = torch.empty(-(-nb // 256), dtype=torch.float32, device=device)
-        offset = torch.empty((), dtype=torch.float32, device=device)
-    else:
-        code2 = absmax2 = offset = None
-        absmax = torch.empty(nb, dtype=torch.float32, device=device)
-    ws_bytes = lib.ct_nf4_quantize_workspace(n, blocksize, int(nested))
-    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
-    with torch.cuda.device(device):
-        status = lib.ct_nf4_quantize(
-            _native.ptr(flat), _native.dtype_code(flat.dtype), n, blocksize, int(nested), _native.ptr(midpoints),
-            _native.ptr(code2), _native.ptr(packed), _native.ptr(absmax), _native.ptr(absmax2), _native.ptr(offset),
-            _native.ptr(workspace), ws_bytes, _native.stream_of(flat))
-    _native.check(status, "ct_nf4_quantize")
-    if nested:
-        state2 = QuantState(absmax2, torch.Size([nb]), code2, 256, "dynamic", torch.float32)
-        state = QuantState(absmax, source.shape, code, blocksize, "nf4", source.dtype, offset, state2)
-    else:
-        state = QuantState(absmax, source.shape, code, blocksize, "nf4", source.dtype)
-    return packed, state
+        status = lib.ct_quantize_blockwise(_native.ptr(first), nb, _native.ptr(offset), _native.ptr(code2),
+                                           _native.ptr(absmax), _native.ptr(absmax2), stream)
+        _native.check(status, "ct_quantize_blockwise")
+    state2 = QuantState(absmax2, torch.Size([nb]), code2, 256, "dynamic", torch.float32)
+    return packed, QuantState(absmax, source.shape, code, blocksize, "nf4", source.dtype, offset, state2)
 
 
 def _quantize_nf4_ops(weight, blocksize=64, compress_statistics=True):
@@ -201,8 +200,7 @@ def _quantize_nf4_ops(weight, blocksize=64, compress_statistics=True):
     packed = ((pairs[:, 0] << 4) | pairs[:, 1]).contiguous().view(-1, 1)
     code = nf4_code(device)
     if compress_statistics:
-        # Mean in float64 so the rounded offset does not depend on reduction order.
-        offset = absmax.double().mean().float()
+        offset = absmax.mean()   # bitsandbytes: torch's fp32 mean of the block absmax
         code2 = dynamic_map().to(device)
         qabs, absmax2 = quantize_blockwise(absmax - offset, code2, 256)
         state2 = QuantState(absmax2, torch.Size([absmax.numel()]), code2, 256, "dynamic", torch.float32)

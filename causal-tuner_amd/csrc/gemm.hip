@@ -1328,7 +1328,7 @@ bool nf4_fusable(const ct_nf4_weight *w) {
 
 using namespace ct;
 
-extern "C" int ct_abi_version(void) { return 7; }
+extern "C" int ct_abi_version(void) { return 8; }
 
 extern "C" const char *ct_status_string(int status) {
     switch (status) {

@@ -199,3 +199,14 @@ extern "C" int ct_nf4_quantize(const void *w, int32_t w_dtype, int64_t n, int32_
     }
     return e == hipSuccess ? 0 : (int)e;
 }
+
+extern "C" int ct_quantize_blockwise(const float *values, int64_t n, const float *offset, const float *code2,
+                                     uint8_t *codes, float *absmax2, hipStream_t stream) {
+    if (n < 0) return -CT_EINVAL_SHAPE;
+    if (n == 0) return 0;
+    if (!values || !offset || !code2 || !codes || !absmax2) return -CT_EINVAL_POINTER;
+    nf4_quantize_nested<<<dim3((unsigned)cdiv(n, 256)), dim3(256), 0, stream>>>(values, n, offset, code2, codes,
+                                                                                 absmax2);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : (int)e;
+}

@@ -17,7 +17,7 @@
  * Reference interfaces (RealJosephus/causal-tuner, paths under src/causal_tuner/):
  *   kernels/nf4_cuda.py:9-43    _decode / dequantize_nf4   -> ct_nf4_dequant
  *   kernels/linear.py:6-13      materialize                -> ct_nf4_dequant
- *   modeling/lora.py:50-55      bitsandbytes quantize_4bit -> ct_nf4_quantize
+ *   modeling/lora.py:50-55      bitsandbytes quantize_4bit -> ct_nf4_quantize (+ ct_quantize_blockwise)
  *   kernels/linear.py:16-24     accumulate                 -> ct_accumulate
  *   kernels/linear.py:27-33     forward_linear             -> ct_forward_linear
  *   kernels/linear.py:36-39     input_gradient             -> ct_input_gradient
@@ -111,6 +111,17 @@ int ct_nf4_dequant(const ct_nf4_weight *w, void *out, int32_t out_dtype, hipStre
  * absmax).
  */
 int64_t ct_nf4_quantize_workspace(int64_t n, int32_t blocksize, int32_t nested);
+/*
+ * Replaces bitsandbytes' quantize_blockwise(absmax - offset, code2, blocksize=256), the
+ * second level of quantize_4bit(compress_statistics=True) (called through Params4bit at
+ * modeling/lora.py:50-55): c = values[i] - offset[0] in fp32; absmax2[j] = max |c| over
+ * block j of 256; codes[i] = the dynamic-map code of c * (1 / absmax2[j]) (bitsandbytes'
+ * binary search and midpoint rule over code2, 256 sorted fp32 values). With ct_nf4_quantize
+ * run with nested = 0 (fp32 absmax) and offset = the caller's fp32 mean of that absmax (as
+ * bitsandbytes computes it, absmax.mean()), the two calls give quantize_4bit's nested state.
+ */
+int ct_quantize_blockwise(const float *values, int64_t n, const float *offset, const float *code2,
+                          uint8_t *codes, float *absmax2, hipStream_t stream);
 int ct_nf4_quantize(const void *w, int32_t w_dtype, int64_t n, int32_t blocksize, int32_t nested,
                     const float *midpoints, const float *code2, uint8_t *packed, void *absmax,
                     float *absmax2, float *offset, void *workspace, int64_t workspace_bytes,

@@ -140,11 +140,13 @@ def dynamic_code(x, code):
     return lower_pivot if x < np.float32((lower + val) * np.float32(0.5)) else pivot
 
 
-def quantize(weight_f32, blocksize=64, nested=True, storage=BF16):
+def quantize(weight_f32, blocksize=64, nested=True, storage=BF16, offset=None):
     """bitsandbytes quantize_4bit(quant_type="nf4", compress_statistics=nested), restated.
 
-    `storage` is the source weight's dtype (QuantState.dtype). Returns (packed uint8
-    [ceil(n/2)], state dict)."""
+    `storage` is the source weight's dtype (QuantState.dtype). bitsandbytes' offset is
+    torch's fp32 mean of the block absmax (absmax.mean()), whose last bits depend on torch's
+    reduction order: pass that value as `offset` to reproduce a state; without it the
+    correctly rounded (float64) mean is used. Returns (packed uint8 [ceil(n/2)], state dict)."""
     flat = np.asarray(weight_f32, dtype=np.float32).reshape(-1)
     n = flat.size
     nb = -(-n // blocksize)
@@ -160,7 +162,7 @@ def quantize(weight_f32, blocksize=64, nested=True, storage=BF16):
     packed = ((codes[0::2] << 4) | codes[1::2]).astype(np.uint8)
     state = {"n": n, "blocksize": blocksize, "nested": nested, "code": NF4_CODE.copy(), "storage": storage}
     if nested:
-        offset = np.float32(absmax.astype(np.float64).mean())
+        offset = np.float32(absmax.astype(np.float64).mean()) if offset is None else np.float32(offset)
         code2 = dynamic_map()
         centred = (absmax - offset).astype(np.float32)
         nb2 = -(-nb // 256)

@@ -138,9 +138,9 @@ def test_full_size_dequant_matches_plain_c_oracle(shape):
     assert err <= 0.2 * w.float().abs().max().item()
 
 
-def _oracle_quantize(values, blocksize, nested):
+def _oracle_quantize(values, blocksize, nested, offset=None):
     return onf4.quantize(values.float().cpu().numpy(), blocksize=blocksize, nested=nested,
-                         storage=NAMES[values.dtype])
+                         storage=NAMES[values.dtype], offset=offset)
 
 
 @pytest.mark.parametrize("shape,blocksize,nested,dtype", [
@@ -161,7 +161,13 @@ def test_device_quantizer_matches_oracle(shape, blocksize, nested, dtype):
         values.view(-1)[blocksize:2 * blocksize] = 0   # an all-zero block (absmax 0, NaN codes)
     packed, state = quantize_nf4(values.cuda(), blocksize=blocksize, compress_statistics=nested)
     torch.cuda.synchronize()
-    want_packed, want = _oracle_quantize(values, blocksize, nested)
+    # the offset is torch's fp32 mean of the block absmax (bitsandbytes' absmax.mean()):
+    # within float rounding of the exact mean; the oracle reproduces the rest from it
+    offset = state.offset.item() if nested else None
+    want_packed, want = _oracle_quantize(values, blocksize, nested, offset)
+    if nested:
+        _, exact = _oracle_quantize(values, blocksize, nested)
+        assert abs(offset - float(exact["offset"])) <= 1e-6 * abs(float(exact["offset"]))
     np.testing.assert_array_equal(packed.cpu().numpy().reshape(-1), want_packed)
     np.testing.assert_array_equal(state.absmax.cpu().numpy(), want["absmax"])
     assert state.blocksize == blocksize and state.dtype == dtype and tuple(state.shape) == shape
@@ -169,9 +175,14 @@ def test_device_quantizer_matches_oracle(shape, blocksize, nested, dtype):
         assert np.float32(state.offset.item()) == want["offset"]
         np.testing.assert_array_equal(state.state2.absmax.cpu().numpy(), want["absmax2"])
         np.testing.assert_array_equal(state.state2.code.cpu().numpy(), want["code2"])
-    # and the host path (torch ops) agrees with the device path
+    # and the host path (torch ops) agrees with the device path (with the host's fp32 mean)
     hp, hs = quantize_nf4(values, blocksize=blocksize, compress_statistics=nested)
-    assert torch.equal(hp, packed.cpu()) and torch.equal(hs.absmax, state.absmax.cpu())
+    assert torch.equal(hp, packed.cpu())
+    if nested:
+        _, host_want = _oracle_quantize(values, blocksize, nested, hs.offset.item())
+        np.testing.assert_array_equal(hs.absmax.numpy(), host_want["absmax"])
+    else:
+        assert torch.equal(hs.absmax, state.absmax.cpu())
 
 
 def test_device_quantizer_round_trip_large():

@@ -117,13 +117,42 @@ def test_dynamic_map_and_binary_search_are_nearest():
         assert abs(float(code[q]) - float(x)) <= np.abs(code.astype(np.float64) - float(x)).min() + 1e-7
 
 
+def test_dynamic_map_is_the_dynamic_tree_data_type():
+    """The second-level code book against the bit-level definition of the dynamic tree data
+    type (Dettmers et al., "8-bit Optimizers via Block-wise Quantization", 2022, sec. 2.1):
+    after the sign bit, the number E of leading zero bits sets the scale 10^-E, the next 1
+    bit is an indicator, and the F = 6 - E remaining bits pick one of 2^F equal bins of
+    [0.1, 1], whose centre is the magnitude; the all-zero magnitude is 0, and the code of
+    negative zero is used for 1.0. Enumerated over all 256 codes in float64 and compared
+    with the linspace construction (fp32) within 2 ulp: any slip in the exponent count, the
+    bins per decade, the bin centres or the signs changes a value by far more."""
+    tree = []
+    for code in range(256):
+        negative, magnitude = code >> 7, code & 127
+        if magnitude == 0:
+            tree.append(1.0 if negative else 0.0)
+            continue
+        e = 7 - magnitude.bit_length()            # leading zeros of the 7-bit magnitude
+        f = 6 - e                                 # fraction bits after the indicator
+        fraction = magnitude & ((1 << f) - 1)
+        value = 10.0 ** -e * (0.1 + (fraction + 0.5) * 0.9 / (1 << f))
+        tree.append(-value if negative else value)
+    tree = np.sort(np.array(tree))
+    code = nf4.dynamic_map().astype(np.float64)
+    assert np.all(np.abs(code - tree) <= 2 * np.spacing(np.abs(tree).astype(np.float32)).astype(np.float64))
+    assert np.count_nonzero(code == 0) == 1 and code[-1] == 1.0
+    for e in range(7):   # 2^(6-e) magnitudes in each decade, on each side
+        inside = (np.abs(code) >= 0.1 * 10.0 ** -e) & (np.abs(code) < 10.0 ** -e)
+        assert np.count_nonzero(inside & (code > 0)) == 2 ** (6 - e) == np.count_nonzero(inside & (code < 0))
+
+
 def test_package_quantizer_matches_the_oracle_bit_for_bit():
     from causal_tuner.quant.nf4 import quantize_nf4, dynamic_map
     np.testing.assert_array_equal(dynamic_map().numpy(), nf4.dynamic_map())
     for shape, bs in (((17, 19), 64), ((130, 256), 64), ((64, 640), 128)):
         w = (torch.randn(shape) * 0.02).to(torch.bfloat16)
         packed, state = quantize_nf4(w, bs)
-        p2, s2 = nf4.quantize(w.float().numpy(), bs, True)
+        p2, s2 = nf4.quantize(w.float().numpy(), bs, True, offset=state.offset.item())
         np.testing.assert_array_equal(packed.numpy().reshape(-1), p2)
         np.testing.assert_array_equal(state.absmax.numpy(), s2["absmax"])
         np.testing.assert_array_equal(state.state2.absmax.numpy(), s2["absmax2"])
