@@ -36,6 +36,21 @@ class NF4Weight(ctypes.Structure):
     ]
 
 
+CT_EPI_NONE, CT_EPI_RESIDUAL, CT_EPI_SILU, CT_EPI_DSILU, CT_EPI_ROPE = 0, 1, 2, 3, 4
+
+
+class Epilogue(ctypes.Structure):
+    """Mirror of `ct_epilogue`: an elementwise step on a projection's bf16 output."""
+
+    _fields_ = [
+        ("kind", _I32), ("trig_dtype", _I32), ("in0", _P), ("ld_in0", _I64), ("in1", _P), ("ld_in1", _I64),
+        ("out0", _P), ("ld_out0", _I64), ("out1", _P), ("ld_out1", _I64), ("cosine", _P), ("sine", _P),
+        ("head_dim", _I64), ("half", _I64),
+    ]
+
+
+_EPI = ctypes.POINTER(Epilogue)
+
 _SIGNATURES = {
     "ct_abi_version": (ctypes.c_int, []),
     "ct_status_string": (ctypes.c_char_p, [ctypes.c_int]),
@@ -44,14 +59,15 @@ _SIGNATURES = {
     "ct_gemm_workspace": (_I64, [_I64, _I64, _I64, _I32, _I32, _I32]),
     "ct_gemm": (ctypes.c_int, [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _P, _I32, _I64, _I64, _I64, _P, _I64,
                                _P]),
+    "ct_gemm_f32": (ctypes.c_int, [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I64, _I64, _P]),
     "ct_forward_linear_workspace": (_I64, [_I64, _I64, _I64, _I64, _I32]),
     "ct_forward_linear": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _P, _I64, _P,
-                                         _I64, _I32, _I64, _I64, _I64, _I64, _P, _I64, _P]),
+                                         _I64, _I32, _I64, _I64, _I64, _I64, _EPI, _P, _I64, _P]),
     "ct_forward_linear_static": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _P, _I64,
-                                                _P, _I64, _I32, _I64, _I64, _I64, _I64, _P]),
+                                                _P, _I64, _I32, _I64, _I64, _I64, _I64, _EPI, _P]),
     "ct_input_gradient_workspace": (_I64, [_I64, _I64, _I64, _I64, _I32]),
     "ct_input_gradient": (ctypes.c_int, [_P, _I64, _P, ctypes.POINTER(NF4Weight), _P, _P, _P, _I64, _P,
-                                         _I64, _I64, _I64, _I64, _I32, _P, _I64, _P]),
+                                         _I64, _I64, _I64, _I64, _I32, _EPI, _P, _I64, _P]),
     "ct_parameter_gradients_workspace": (_I64, [_I64, _I64, _I64, _I64]),
     "ct_parameter_gradients": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64,
                                               _I64, _I32, _P, _I64, _P]),
@@ -83,7 +99,7 @@ EXPORTED = tuple(_SIGNATURES)
 _library = None
 
 
-ABI_VERSION = 8   # ct_abi_version() of the library these signatures describe
+ABI_VERSION = 10   # ct_abi_version() of the library these signatures describe
 
 
 def library_path():
@@ -152,6 +168,33 @@ def nf4_kind(desc):
     if desc is None:
         return 0
     return 1 if desc.nested else 2
+
+
+def _matrix(t, rows):
+    """(pointer, row pitch) of a bf16 tensor viewed as [rows, width] with unit stride."""
+    view = t.reshape(rows, -1) if t.dim() != 2 else t
+    if view.stride(-1) != 1:
+        raise ValueError("epilogue tensors need unit stride along a row")
+    return view.data_ptr(), max(view.stride(0), view.shape[1])
+
+
+def epilogue(kind, rows, in0=None, in1=None, out0=None, out1=None, rotary=None):
+    """A ct_epilogue for an output of `rows` rows; `rotary` is (cosine, sine, head_dim)
+    with cosine/sine [rows, half] contiguous."""
+    e = Epilogue(kind=kind)
+    for name, t in (("in0", in0), ("in1", in1), ("out0", out0), ("out1", out1)):
+        if t is not None:
+            if t.dtype != torch.bfloat16:
+                raise ValueError("epilogue tensors are bfloat16")
+            ptr, ld = _matrix(t, rows)
+            setattr(e, name, ptr)
+            setattr(e, "ld_" + name, ld)
+    if rotary is not None:
+        cosine, sine, head_dim = rotary
+        e.cosine, e.sine = cosine.data_ptr(), sine.data_ptr()
+        e.trig_dtype = dtype_code(cosine.dtype)
+        e.head_dim, e.half = int(head_dim), int(cosine.shape[-1])
+    return e
 
 
 def nf4_descriptor(weight, state):

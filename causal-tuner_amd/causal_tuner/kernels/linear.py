@@ -39,6 +39,10 @@ def _unsupported(what, *tensors):
     raise NotImplementedError(f"{what}: the HIP path computes in bfloat16 on the device (got {', '.join(dtypes)})")
 
 
+def _device_f32(*tensors):
+    return all(t.is_cuda and t.dtype == torch.float32 for t in tensors if t is not None)
+
+
 def _aligned(t):
     return t.data_ptr() % 16 == 0
 
@@ -65,6 +69,15 @@ def _operand(t):
         return t, t.stride(1), 1
     t = t.contiguous()
     return t, max(t.shape[1], 1), 0
+
+
+def fusable(*tensors):
+    """Whether a fused GEMM epilogue may write/read these and any window of their rows:
+    device bf16 matrices with unit stride along their rows, a row pitch of a multiple of 8
+    elements and a 16-byte aligned start (None entries are ignored)."""
+    return all(t.is_cuda and t.dtype == torch.bfloat16 and t.dim() == 2 and t.stride(1) == 1
+               and t.stride(0) >= t.shape[1] and t.stride(0) % 8 == 0 and _aligned(t)
+               for t in tensors if t is not None)
 
 
 def _workspace(nbytes, device):
@@ -94,6 +107,62 @@ class _Contiguous(_Output):
         self.buffer = target if target.is_contiguous() else torch.empty(target.shape, dtype=target.dtype,
                                                                         device=target.device)
         self.ld = max(target.shape[-1], 1)
+
+
+def _f32_operand(t):
+    """(tensor, ld, transposed) for a float32 matrix view: stored row-major (0) or as the
+    row-major transpose (1); anything else is copied."""
+    rows, cols = t.shape
+    if t.stride(1) == 1 and t.stride(0) >= max(cols, 1):
+        return t, max(t.stride(0), 1), 0
+    if t.stride(0) == 1 and t.stride(1) >= max(rows, 1):
+        return t, max(t.stride(1), 1), 1
+    t = t.contiguous()
+    return t, max(cols, 1), 0
+
+
+def mm_f32(left, right, out, *, add=False, bias=None):
+    """out (+)= left right (+ bias) in float32 on the device (ct_gemm_f32: fp32 MFMA
+    products and sums): the torch.mm / addmm of the reference's float32 compute dtype
+    (kernels/linear.py:16-44). `left` [m, k] and `right` [k, n] may be transposed views."""
+    m, k = left.shape
+    n = right.shape[1]
+    if right.shape[0] != k or tuple(out.shape) != (m, n):
+        raise ValueError(f"mm_f32: {tuple(left.shape)} x {tuple(right.shape)} -> {tuple(out.shape)}")
+    if not _device_f32(left, right, out, bias):
+        _unsupported("mm_f32", left, right, out, bias)
+    lt, ldl, tl = _f32_operand(left)
+    rt, ldr, tr = _f32_operand(right)
+    bias = None if bias is None else bias.contiguous()
+    direct = out.stride(1) == 1 and out.stride(0) >= max(n, 1)
+    target = out if direct else (out.contiguous() if add else torch.empty((m, n), dtype=out.dtype,
+                                                                          device=out.device))
+    with _native.device_of(out):
+        status = _native.library().ct_gemm_f32(
+            _native.ptr(lt), ldl, tl, _native.ptr(rt), ldr, tr, _native.ptr(target), max(target.stride(0), 1),
+            int(add), _native.ptr(bias), m, n, k, _native.stream_of(out))
+    _native.check(status, "ct_gemm_f32")
+    if target is not out:
+        out.copy_(target)
+
+
+def _mm_bf16(left, right, out, *, add=False):
+    """out = bf16(left right (+ out)) through ct_gemm (fp32 accumulation, one rounding)."""
+    m, k = left.shape
+    n = right.shape[1]
+    lt, ldl, tl = _operand(left)
+    rt, ldr, tr = _operand(right)
+    target = _Output(out)
+    if add and target.buffer is not out:
+        target.buffer.copy_(out)
+    lib = _native.library()
+    ws = _workspace(lib.ct_gemm_workspace(m, n, k, tl, tr, _native.CT_BF16), out.device)
+    with _native.device_of(out):
+        status = lib.ct_gemm(_native.ptr(lt), ldl, tl, _native.ptr(rt), ldr, tr, _native.ptr(target.buffer),
+                             target.ld, _native.CT_BF16, None, int(add), m, n, k, _native.ptr(ws), ws.numel(),
+                             _native.stream_of(out))
+    _native.check(status, "ct_gemm")
+    target.finish()
 
 
 # ----------------------------------------------------------------------------- operators
@@ -182,6 +251,13 @@ def accumulate(output, left, right, *, add=True):
         _native.check(status, "ct_accumulate")
         if target.buffer is not output:
             output.copy_(target.buffer + output if add else target.buffer)
+    elif output.is_cuda:
+        if _device_f32(output, left, right):
+            mm_f32(left, right, output, add=add)
+        elif _device_bf16(output, left, right):
+            _mm_bf16(left, right, output, add=add)   # bf16 parameters: one rounding of acc (+ out)
+        else:
+            _unsupported("accumulate", output, left, right)
     elif output.dtype != left.dtype:
         output.addmm_(left.to(output.dtype), right.to(output.dtype), beta=beta)
     else:
@@ -200,14 +276,21 @@ def forward_linear(x, weight, a, b, *, out, xa, bias=None):
         torch.mm(x, a.T, out=xa)
         out.addmm_(xa, b.T)
         return
+    if _device_f32(x, weight, a, b, out, xa, bias):
+        # the reference's three products in float32 (kernels/linear.py:28-33)
+        mm_f32(x, weight.T, out, bias=bias)
+        mm_f32(x, a.T, xa)
+        mm_f32(xa, b.T, out, add=True)
+        return
     if not _device_bf16(x, weight, a, b, out, xa, bias):
         _unsupported("forward_linear", x, weight, a, b, out, xa, bias)
     _forward(x, weight, None, a, b, bias, out, xa)
 
 
-def _forward(x, weight, state, a, b, bias, out, xa, xa_given=False):
+def _forward(x, weight, state, a, b, bias, out, xa, xa_given=False, epilogue=None):
     """ct_forward_linear; with xa_given, xa (a row-major view, e.g. a column slice of a
-    group's shared x [a_1; a_2; ...]^T) already holds x a^T and is only read."""
+    group's shared x [a_1; a_2; ...]^T) already holds x a^T and is only read. `epilogue`
+    (a _native.Epilogue over `out`'s rows) is applied to the output in the GEMM."""
     m, k = x.shape
     n, r = out.shape[1], a.shape[0]
     x, ldx = _rows(x)
@@ -215,6 +298,8 @@ def _forward(x, weight, state, a, b, bias, out, xa, xa_given=False):
     a, b = a.contiguous(), b.contiguous()
     bias = None if bias is None else bias.contiguous()
     target, low = _Output(out), _Output(xa)
+    if epilogue is not None and target.buffer is not out:
+        raise ValueError("a fused epilogue needs a unit-stride, 16-byte aligned output")
     if xa_given and low.buffer is not xa:
         low.buffer.copy_(xa)
     desc = None if state is None else _native.nf4_descriptor(w, state)
@@ -224,7 +309,8 @@ def _forward(x, weight, state, a, b, bias, out, xa, xa_given=False):
         status = lib.ct_forward_linear(
             _native.ptr(x), ldx, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),
             _native.ptr(b), _native.ptr(bias), _native.ptr(target.buffer), target.ld, _native.ptr(low.buffer),
-            low.ld, int(bool(xa_given)), m, n, k, r, _native.ptr(ws), ws.numel(), _native.stream_of(x))
+            low.ld, int(bool(xa_given)), m, n, k, r, None if epilogue is None else ctypes.byref(epilogue),
+            _native.ptr(ws), ws.numel(), _native.stream_of(x))
     _native.check(status, "ct_forward_linear")
     target.finish()
     if not xa_given:
@@ -240,18 +326,26 @@ def input_gradient(dy, weight, a, b, dx, low, *, add=False):
         torch.addmm(dx, dy, weight, beta=1 if add else 0, out=dx)
         dx.addmm_(low, a)
         return
+    if _device_f32(dy, weight, a, b, dx, low):
+        # kernels/linear.py:36-39 in float32
+        mm_f32(dy, b, low)
+        mm_f32(dy, weight, dx, add=add)
+        mm_f32(low, a, dx, add=True)
+        return
     if not _device_bf16(dy, weight, a, b, dx, low):
         _unsupported("input_gradient", dy, weight, a, b, dx, low)
     _input_gradient(dy, weight, None, a, b, dx, low, add)
 
 
-def _input_gradient(dy, weight, state, a, b, dx, low, add):
+def _input_gradient(dy, weight, state, a, b, dx, low, add, epilogue=None):
     m, n = dy.shape
     k, r = dx.shape[1], a.shape[0]
     dy, lddy = _rows(dy)
     w = None if weight is None else weight.contiguous()
     a, b = a.contiguous(), b.contiguous()
     target, lowc = _Output(dx), _Contiguous(low)
+    if epilogue is not None and (target.buffer is not dx or add):
+        raise ValueError("a fused epilogue needs add=False and a unit-stride, 16-byte aligned dx")
     if add and target.buffer is not dx:
         target.buffer.copy_(dx)
     desc = None if state is None else _native.nf4_descriptor(w, state)
@@ -261,7 +355,7 @@ def _input_gradient(dy, weight, state, a, b, dx, low, add):
         status = lib.ct_input_gradient(
             _native.ptr(dy), lddy, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),
             _native.ptr(b), _native.ptr(target.buffer), target.ld, _native.ptr(lowc.buffer), m, n, k, r, int(add),
-            _native.ptr(ws), ws.numel(), _native.stream_of(dy))
+            None if epilogue is None else ctypes.byref(epilogue), _native.ptr(ws), ws.numel(), _native.stream_of(dy))
     _native.check(status, "ct_input_gradient")
     target.finish()
     lowc.finish()
@@ -328,16 +422,22 @@ class _Base:
             self.matrix = materialize(weight, state, dtype)
         self.rows = int(state.shape[0]) if state is not None else len(weight)
 
-    def forward(self, x, a, b, bias, out, xa, xa_given=False):
-        if xa_given:   # device path only: xa holds x a^T already
-            _forward(x, self.matrix if self.state is None else self.weight, self.state, a, b, bias, out, xa, True)
+    def forward(self, x, a, b, bias, out, xa, xa_given=False, epilogue=None):
+        """out = x w^T + (x a^T) b^T (+ bias). Device only: with xa_given, xa holds x a^T
+        already; `epilogue` is an elementwise step fused into the output."""
+        if xa_given or epilogue is not None:
+            _forward(x, self.matrix if self.state is None else self.weight, self.state, a, b, bias, out, xa,
+                     xa_given, epilogue)
         elif self.state is None:
             forward_linear(x, self.matrix, a, b, bias=bias, out=out, xa=xa)
         else:
             _forward(x, self.weight, self.state, a, b, bias, out, xa)
 
-    def input_gradient(self, dy, a, b, dx, low, add):
-        if self.state is None:
+    def input_gradient(self, dy, a, b, dx, low, add, epilogue=None):
+        if epilogue is not None:
+            _input_gradient(dy, self.matrix if self.state is None else self.weight, self.state, a, b, dx, low, add,
+                            epilogue)
+        elif self.state is None:
             input_gradient(dy, self.matrix, a, b, dx, low, add=add)
         else:
             _input_gradient(dy, self.weight, self.state, a, b, dx, low, add)
@@ -415,23 +515,42 @@ class _LoRAGroup(torch.autograd.Function):
         # slices of one buffer so a stacked GEMM fills them together.
         xa = torch.empty((len(flat) if keep else span, sum(ranks)), device=x.device, dtype=dtype)
         columns = [xa[:, sum(ranks[:i]):sum(ranks[:i+1])] for i in range(count)]
+        # The rotation of q/k (core_cuda.py:192-200) and the residual add (linear.py:90-91)
+        # run in the GEMM epilogue when the operands allow it, else as separate passes.
+        rotated = min(count, 2) if head_dim else 0
+        trig = None
+        if rotated:
+            half = cosine.shape[-1]
+            trig = tuple(value.reshape(-1, half) if value.numel() == len(flat) * half else None
+                         for value in (cosine, sine))
+        rope_fused = bool(rotated) and trig[0] is not None and trig[1] is not None and \
+            fusable(*outputs[:rotated]) and all(out.shape[1] % head_dim == 0 for out in outputs[:rotated])
+        residual_flat = None if residual is None else residual.reshape(len(flat), -1)
+        residual_fused = residual_flat is not None and not rotated and fusable(outputs[0], residual_flat)
         for start in range(0, len(flat), step):
             part = flat[start:start+step]
             rows = slice(start, start+len(part)) if keep else slice(0, len(part))
+            window = slice(start, start+len(part))
             if stack is not None:
                 _low_rank(part, stack, xa[rows], transpose=True)
             for index, base in enumerate(bases):
-                base.forward(part, factors[2*index], factors[2*index+1], biases[index],
-                             outputs[index][start:start+len(part)], columns[index][rows], xa_given=stack is not None)
+                epilogue = None
+                if rope_fused and index < rotated:
+                    epilogue = _native.epilogue(_native.CT_EPI_ROPE, len(part),
+                                                rotary=(trig[0][window], trig[1][window], head_dim))
+                elif residual_fused and index == 0:
+                    epilogue = _native.epilogue(_native.CT_EPI_RESIDUAL, len(part), in0=residual_flat[window])
+                base.forward(part, factors[2*index], factors[2*index+1], biases[index], outputs[index][window],
+                             columns[index][rows], xa_given=stack is not None, epilogue=epilogue)
         kept = columns if keep else []
         ctx.kept = len(kept)
         ctx.save_for_backward(x, cosine, sine, *parameters, *kept)
         del factors, stack, bases, xa, columns, kept
         outputs = [out.reshape(*x.shape[:-1], out.shape[1]) for out in outputs]
-        if head_dim:
+        if rotated and not rope_fused:
             from .core_cuda import rotate_owned_qk
             rotate_owned_qk(outputs[0], outputs[1], cosine, sine, head_dim)
-        if residual is not None:
+        if residual is not None and not residual_fused:
             outputs[0].add_(residual)
         return tuple(outputs)
 
@@ -494,6 +613,9 @@ def _low_rank(x, factor, out, *, transpose):
     the reference (linear.py:124-125, mlp_cuda.py:134,140)."""
     if not x.is_cuda:
         torch.mm(x, factor.T if transpose else factor, out=out)
+        return
+    if _device_f32(x, factor, out):
+        mm_f32(x, factor.T if transpose else factor, out)
         return
     if not _device_bf16(x, factor, out):
         _unsupported("low-rank product", x, factor, out)

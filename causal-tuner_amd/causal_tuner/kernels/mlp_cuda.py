@@ -26,7 +26,7 @@ results into separate tile buffers so the kept values survive a repeated backwar
 import torch
 
 from . import _native
-from .linear import _Base, _low_rank, forward_linear, group_factors, input_gradient, parameter_gradients, \
+from .linear import _Base, _low_rank, forward_linear, fusable, group_factors, input_gradient, parameter_gradients, \
     projection_parameters
 
 
@@ -103,23 +103,32 @@ class _MLPProjections:
             return pair, (pair[:, :self.rank[GATE]], pair[:, self.rank[GATE]:])
         return None, (self.empty(rows, self.rank[GATE]), self.empty(rows, self.rank[UP]))
 
-    def project(self, which, x, out, xa):
-        """out = x w^T + (x a^T) b^T for one projection, xa = x a^T written."""
-        forward_linear(x, self.bases[which], self.a[which], self.b[which], out=out, xa=xa)
+    def project(self, which, x, out, xa, epilogue=None):
+        """out = x w^T + (x a^T) b^T for one projection, xa = x a^T written; `epilogue` an
+        elementwise step fused into the GEMM's output."""
+        if epilogue is None:
+            forward_linear(x, self.bases[which], self.a[which], self.b[which], out=out, xa=xa)
+        else:
+            self.bases[which].forward(x, self.a[which], self.b[which], None, out, xa, epilogue=epilogue)
 
-    def gate_up(self, x, gate, up, pair, xa):
-        """gate and up of one tile. With the stacked factors their xa come from one GEMM
-        into `pair` (whose column halves are xa) and the projections read them."""
+    def gate_up(self, x, gate, up, pair, xa, epilogue=None):
+        """gate and up of one tile (`epilogue` applies to up's output, which gate precedes).
+        With the stacked factors their xa come from one GEMM into `pair` (whose column
+        halves are xa) and the projections read them."""
         if self.stacked is None or not len(x):
             self.project(GATE, x, gate, xa[GATE])
-            self.project(UP, x, up, xa[UP])
+            self.project(UP, x, up, xa[UP], epilogue)
             return
         _low_rank(x, self.stacked, pair, transpose=True)
         for which, out in ((GATE, gate), (UP, up)):
-            self.bases[which].forward(x, self.a[which], self.b[which], None, out, xa[which], xa_given=True)
+            self.bases[which].forward(x, self.a[which], self.b[which], None, out, xa[which], xa_given=True,
+                                      epilogue=epilogue if which == UP else None)
 
-    def input_gradient(self, which, dy, dx, low, add):
-        input_gradient(dy, self.bases[which], self.a[which], self.b[which], dx, low, add=add)
+    def input_gradient(self, which, dy, dx, low, add, epilogue=None):
+        if epilogue is None:
+            input_gradient(dy, self.bases[which], self.a[which], self.b[which], dx, low, add=add)
+        else:
+            self.bases[which].input_gradient(dy, self.a[which], self.b[which], dx, low, add, epilogue)
 
     def low_product(self, which, dy, low):
         """low = dy b, when the input gradient is not needed."""
@@ -148,11 +157,16 @@ def _forward_into(output, x, dtype, tile, states, parameters, residual, *, save=
     else:
         gate_tile, up_tile = mlp.empty(span, mlp.width), mlp.empty(span, mlp.width)
         pair_tile, xa_tile = mlp.xa_buffer(span)
+    # SiLU x up runs in the up GEMM's epilogue (the raw up kept beside h in cache mode) and
+    # the residual add in the down GEMM's, when the buffers allow it.
+    fused = fusable(target, flat, *((gate_all, up_all, hidden_tile) if save else (gate_tile, up_tile)))
+    residual_flat = None if residual is None else residual.reshape(rows, -1)
+    residual_fused = residual_flat is not None and fused and fusable(residual_flat)
     for start in _tile_starts(rows, tile):
         part = flat[start:start + tile]
         n = len(part)
+        window = slice(start, start + n)
         if save:
-            window = slice(start, start + n)
             gate, up = gate_all[window], up_all[window]
             pair = None if pair_all is None else pair_all[window]
             xa = tuple(value[window] for value in xa_all)
@@ -161,11 +175,19 @@ def _forward_into(output, x, dtype, tile, states, parameters, residual, *, save=
             gate, up = gate_tile[:n], up_tile[:n]
             pair = None if pair_tile is None else pair_tile[:n]
             xa = tuple(value[:n] for value in xa_tile)
-            hidden = gate   # h overwrites the tile's gate, which is not needed after it
-        mlp.gate_up(part, gate, up, pair, xa)
-        activation(gate, up, out=hidden)
-        mlp.project(DOWN, hidden, target[start:start + n], xa_down[:n])
-    if residual is not None:
+            # h overwrites the tile's up (fused) or gate, neither needed after it
+            hidden = up if fused else gate
+        if fused:
+            # up's GEMM writes h; in cache mode its raw output goes to the kept up
+            silu = _native.epilogue(_native.CT_EPI_SILU, n, in0=gate, out0=up if save else None)
+            mlp.gate_up(part, gate, hidden if save else up, pair, xa, silu)
+        else:
+            mlp.gate_up(part, gate, up, pair, xa)
+            activation(gate, up, out=hidden)
+        add = (_native.epilogue(_native.CT_EPI_RESIDUAL, n, in0=residual_flat[window]) if residual_fused
+               else None)
+        mlp.project(DOWN, hidden, target[window], xa_down[:n], add)
+    if residual is not None and not residual_fused:
         output.add_(residual)
     return (gate_all, up_all, *xa_all) if save else ()
 
@@ -187,6 +209,8 @@ def _backward(ctx, grad, x, kept, parameters):
     low = mlp.empty(span, max(mlp.rank))
     xa_down = mlp.empty(span, mlp.rank[DOWN])
     pair_tile, xa_tile = (None, None) if kept else mlp.xa_buffer(span)
+    # The SiLU backward runs in the epilogue of down's input-gradient GEMM when it can.
+    fused = fusable(flat, first, *kept[:2])
     for start in _tile_starts(rows, tile):
         part, dy = flat[start:start + tile], upstream[start:start + tile]
         n = len(part)
@@ -197,12 +221,15 @@ def _backward(ctx, grad, x, kept, parameters):
         else:
             xa = tuple(value[:n] for value in xa_tile)
             mlp.gate_up(part, d_gate, d_up, None if pair_tile is None else pair_tile[:n], xa)
-        mlp.input_gradient(DOWN, dy, d_hidden, low[:n, :mlp.rank[DOWN]], False)
-        if kept:
-            # Read the kept gate/up, write d gate / d up into the tile buffers and h over dh.
-            _silu_kernel(kept[0][window], kept[1][window], d_hidden, d_gate, d_up, backward=True, reconstruct=True)
-        else:
-            activation(d_gate, d_up, d_hidden)
+        # dh, then (gate, up, dh) -> (d gate, d up, h): the tile buffers receive d gate and
+        # d up (in place of the recomputed gate/up, or beside the kept ones) and h lands
+        # over dh; fused into the dh GEMM's epilogue when the buffers allow it.
+        gate, up = (kept[0][window], kept[1][window]) if kept else (d_gate, d_up)
+        dsilu = (_native.epilogue(_native.CT_EPI_DSILU, n, in0=gate, in1=up, out0=d_gate, out1=d_up) if fused
+                 else None)
+        mlp.input_gradient(DOWN, dy, d_hidden, low[:n, :mlp.rank[DOWN]], False, dsilu)
+        if not fused:
+            _silu_kernel(gate, up, d_hidden, d_gate, d_up, backward=True, reconstruct=True)
         hidden = d_hidden
         _low_rank(hidden, mlp.a[DOWN], xa_down[:n], transpose=True)
         parameter_gradients(hidden, dy, *grads[DOWN], low[:n, :mlp.rank[DOWN]], xa_down[:n], add=start > 0)

@@ -13,7 +13,7 @@
 // each element is read completely before any of its outputs is written, so that is safe.
 // Elementwise and HBM-bound: 8 elements per lane per step with 16-byte accesses.
 
-#include "common.hpp"
+#include "epilogue.hpp"
 
 namespace ct {
 namespace {
@@ -25,12 +25,6 @@ __device__ __forceinline__ float load_t(const void *p, int64_t i) {
 }
 
 template <int T>
-__device__ __forceinline__ float round_t(float v) {
-    if constexpr (T == CT_BF16) return bf16_to_f32(bf16_bits(v));
-    else return v;
-}
-
-template <int T>
 __device__ __forceinline__ void store_t(void *p, int64_t i, float v) {
     if constexpr (T == CT_BF16) static_cast<uint16_t *>(p)[i] = bf16_bits(v);
     else static_cast<float *>(p)[i] = v;
@@ -39,17 +33,15 @@ __device__ __forceinline__ void store_t(void *p, int64_t i, float v) {
 template <int T, bool BACKWARD, bool RECONSTRUCT>
 __device__ __forceinline__ void element(const void *gate, const void *up, void *h, void *dg, void *du, int64_t i) {
     const float g = load_t<T>(gate, i), u = load_t<T>(up, i);
-    const float sig = 1.f / (1.f + expf(-g));
-    const float act = round_t<T>(g * sig);
     if constexpr (BACKWARD) {
-        const float grad = load_t<T>(h, i);
-        const float pg = round_t<T>(grad * u);
-        const float dgate = pg * (sig * (1.f + g * (1.f - sig)));
-        const float dup = grad * act;
+        float dgate, dup, hidden;
+        silu_backward<T>(g, u, load_t<T>(h, i), dgate, dup, hidden);
         store_t<T>(dg, i, dgate);
         store_t<T>(du, i, dup);
+        if constexpr (RECONSTRUCT) store_t<T>(h, i, hidden);
+    } else {
+        store_t<T>(h, i, silu_forward<T>(g, u));
     }
-    if constexpr (RECONSTRUCT) store_t<T>(h, i, act * u);
 }
 
 // bf16, 16-byte aligned, n % 8 == 0: one 16-byte load or store per operand per lane.
@@ -68,15 +60,8 @@ __global__ __launch_bounds__(256) void silu_multiply_vec(const uint4 *gate, cons
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const float g = bf16_to_f32(g16[j]), u = bf16_to_f32(u16[j]);
-        const float sig = 1.f / (1.f + expf(-g));
-        const float act = bf16_to_f32(bf16_bits(g * sig));
-        if constexpr (BACKWARD) {
-            const float grad = bf16_to_f32(h16[j]);
-            const float pg = bf16_to_f32(bf16_bits(grad * u));
-            o_dg[j] = pg * (sig * (1.f + g * (1.f - sig)));
-            o_du[j] = grad * act;
-        }
-        o_h[j] = act * u;
+        if constexpr (BACKWARD) silu_backward<CT_BF16>(g, u, bf16_to_f32(h16[j]), o_dg[j], o_du[j], o_h[j]);
+        else o_h[j] = silu_forward<CT_BF16>(g, u);
     }
     auto pack = [](const float (&v)[8]) {
         return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),

@@ -701,6 +701,52 @@ struct FastRunner {
 };
 
 // ------------------------------------------------------------------------- the kernel body
+
+// The elementwise step (epilogue.hpp) over a bf16 output tile staged in LDS: rows
+// [0, BM/2) in lo, [BM/2, BM) in hi, BN values per row. The workgroup walks the tile in
+// 16-byte runs, consecutive threads along a row, so every side input and output access is
+// coalesced; each thread reads the side inputs of U runs before it applies and stores any.
+template <int KIND, int BM, int BN, int THREADS, bool VEC>
+__device__ __forceinline__ void epilogue_tile(const GemmParams &p, const uint16_t *lo, const uint16_t *hi, int tid,
+                                              int64_t m0, int64_t n0, int64_t ncols, uint16_t *c) {
+    constexpr int kRuns = BM * (BN / 8), kPer = kRuns / THREADS, U = kPer < 8 ? kPer : 8;
+    static_assert(kRuns % (THREADS * U) == 0, "whole batches of runs");
+    for (int base = tid; base < kRuns; base += THREADS * U) {
+        EpiSide<8> side[U];
+        float y[U][8];
+        int64_t row[U], col[U];
+        int count[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int run = base + u * THREADS, lr = run / (BN / 8), lc = (run % (BN / 8)) * 8;
+            row[u] = m0 + lr;
+            col[u] = n0 + lc;
+            count[u] = (row[u] < p.m && col[u] < ncols) ? (ncols - col[u] < 8 ? (int)(ncols - col[u]) : 8) : 0;
+            if (count[u] <= 0) continue;
+            epilogue_load<KIND, 8>(p.epi, row[u], col[u], count[u], side[u]);
+            const uint16_t *src = (lr < BM / 2 ? lo + lr * BN : hi + (lr - BM / 2) * BN) + lc;
+            const uint4 q = *reinterpret_cast<const uint4 *>(src);
+            const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) y[u][j] = pair_value(w[j / 2], j & 1);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (count[u] <= 0) continue;
+            epilogue_apply<KIND, 8>(p.epi, row[u], col[u], count[u], side[u], y[u]);
+            uint16_t *out = c + row[u] * p.ldc + col[u];
+            if (VEC && count[u] == 8) {
+                *reinterpret_cast<uint4 *>(out) = make_uint4(pack_bf16x2(y[u][0], y[u][1]), pack_bf16x2(y[u][2], y[u][3]),
+                                                             pack_bf16x2(y[u][4], y[u][5]), pack_bf16x2(y[u][6], y[u][7]));
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (j < count[u]) out[j] = bf16_bits(y[u][j]);
+            }
+        }
+    }
+}
+
 template <int BM, int BN, int A0, int B0, int A1, int B1, int MODE, int OUT, int WAVES_M = 2, int WAVES_N = 2>
 __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     constexpr bool VEC = MODE != 0;
@@ -815,6 +861,51 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) bias[j] = (p.bias && col + j < ncols) ? bf16_to_f32(p.bias[col + j]) : 0.f;
     const bool full = col + FN <= ncols;
+    if constexpr (OUT == CT_BF16) {
+        if (p.epi.kind != CT_EPI_NONE && !p.beta) {
+            // Stage the rounded tile in LDS (the operand buffers are free once every wave
+            // has left the main loop), then run the step over it in coalesced runs.
+            static_assert((BM + BN) * 8 * 16 >= BM * BN, "half a bf16 tile fits one operand buffer");
+            static_assert(WM <= BM / 2 && (BM / 2) % WM == 0, "a wave's rows stay inside one half");
+            __syncthreads();
+            uint16_t *lo = reinterpret_cast<uint16_t *>(lds0), *hi = reinterpret_cast<uint16_t *>(lds1);
+            uint16_t *mine = wm0 < BM / 2 ? lo : hi;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int lr = (wm0 % (BM / 2)) + i * 16 + (lane >> 4) * 4 + e;
+                    uint32_t w[FN / 2];
+#pragma unroll
+                    for (int j = 0; j < FN / 2; ++j)
+                        w[j] = pack_bf16x2(acc[i][2 * j][e] + bias[2 * j], acc[i][2 * j + 1][e] + bias[2 * j + 1]);
+                    uint16_t *dst = mine + lr * BN + wn0 + (lane & 15) * FN;
+                    if constexpr (FN == 8) *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+                    else if constexpr (FN == 4) *reinterpret_cast<uint2 *>(dst) = make_uint2(w[0], w[1]);
+                    else *reinterpret_cast<uint32_t *>(dst) = w[0];
+                }
+            __syncthreads();
+            constexpr int kThreadsWg = WAVES_M * WAVES_N * 64;
+            uint16_t *c = static_cast<uint16_t *>(p.c) + out_shift;
+            switch (p.epi.kind) {
+                case CT_EPI_RESIDUAL:
+                    epilogue_tile<CT_EPI_RESIDUAL, BM, BN, kThreadsWg, VEC>(p, lo, hi, tid, m0, n0, ncols, c);
+                    break;
+                case CT_EPI_SILU:
+                    epilogue_tile<CT_EPI_SILU, BM, BN, kThreadsWg, VEC>(p, lo, hi, tid, m0, n0, ncols, c);
+                    break;
+                case CT_EPI_DSILU:
+                    epilogue_tile<CT_EPI_DSILU, BM, BN, kThreadsWg, VEC>(p, lo, hi, tid, m0, n0, ncols, c);
+                    break;
+                case CT_EPI_ROPE:
+                    epilogue_tile<CT_EPI_ROPE, BM, BN, kThreadsWg, VEC>(p, lo, hi, tid, m0, n0, ncols, c);
+                    break;
+                default:
+                    break;
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -890,7 +981,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 }
 
 template <int BM, int BN, int A0, int B0, int A1, int B1, int MODE, int OUT>
-__global__ __launch_bounds__(kThreads) void gemm_small(const GemmParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_small(const GemmParams p) {
     gemm_body<BM, BN, A0, B0, A1, B1, MODE, OUT>(p);
 }
 
@@ -1130,6 +1221,36 @@ int64_t total_tiles(const GemmParams &p) {
 #define CT_LAYOUT(a0, b0, a1, b1) \
     (((a0) << 12) | ((b0) << 8) | ((a1) << 4) | (b1))
 
+// Split count of the mid-size route (65..511 rows: fp32 split partials of the 256 x 256
+// runner, then a reduction), or 1 when the problem does not take it.
+int mid_split_route(const Problem &pr) {
+    const GemmParams &p = pr.p;
+    if (pr.splits != 1 || pr.out != CT_BF16 || p.group_tiles != 0 || p.m <= 64) return 1;
+    const int splits = mid_splits(p.m, p.n, p.seg[0].k + (p.nseg > 1 ? p.seg[1].k : 0));
+    const int64_t need = (int64_t)splits * p.m * p.n * 4;
+    return (splits > 1 && fast_ok(pr) && pr.ws && pr.ws_bytes >= need && aligned16(pr.ws) && p.n % 8 == 0) ? splits
+                                                                                                           : 1;
+}
+
+// Whether the problem's epilogue runs inside the GEMM (epilogue_tile over the LDS-staged
+// output tile) rather than as a pass over the finished output. The split and few-row
+// routes always pass afterwards. So do the SiLU steps on 256 x 256 tiles: one workgroup
+// fills a CU there, so their two or three extra tensor streams would run with the MFMA
+// units idle, after every tile at once (measured slower than the separate pass at 4096 x
+// 8192), while the 128 x 128 tiles run two workgroups per CU and overlap one's step with
+// the other's products.
+bool epilogue_fused(const Problem &pr) {
+    const GemmParams &p = pr.p;
+    if (mid_split_route(pr) > 1) return false;
+    if (pr.splits == 1 && pr.out == CT_BF16 && p.m <= 64) {
+        const int sa[2] = {pr.src[0], p.nseg > 1 ? pr.src[2] : pr.src[0]};
+        const int sb[2] = {pr.src[1], p.nseg > 1 ? pr.src[3] : pr.src[1]};
+        if (skinny_supported(p, sa, sb, pr.out)) return false;
+    }
+    const int tile = pr.tile >= 0 ? pr.tile : choose_tile(p.m, p.n, pr.splits);
+    return !(tile == TILE_256 && (p.epi.kind == CT_EPI_SILU || p.epi.kind == CT_EPI_DSILU));
+}
+
 hipError_t run(Problem &pr, hipStream_t s) {
     GemmParams &p = pr.p;
     if (p.m == 0 || p.n == 0) return hipSuccess;
@@ -1137,27 +1258,44 @@ hipError_t run(Problem &pr, hipStream_t s) {
         pr.src[2] = pr.src[0];
         pr.src[3] = pr.src[1];
     }
-    if (pr.splits == 1 && pr.out == CT_BF16 && p.group_tiles == 0 && p.m > 64) {
-        const int splits = mid_splits(p.m, p.n, p.seg[0].k + (p.nseg > 1 ? p.seg[1].k : 0));
-        const int64_t need = (int64_t)splits * p.m * p.n * 4;
-        if (splits > 1 && fast_ok(pr) && pr.ws && pr.ws_bytes >= need && aligned16(pr.ws) && p.n % 8 == 0) {
-            Problem q = pr;
-            q.splits = splits;
-            q.out = CT_F32;
-            q.tile = TILE_256;
-            q.ws = nullptr;
-            q.ws_bytes = 0;
-            q.p.c = pr.ws;
-            q.p.ldc = p.n;
-            q.p.split_stride = p.m * p.n;
-            q.p.beta = 0;
-            q.p.bias = nullptr;
-            const hipError_t e = run(q, s);
-            if (e != hipSuccess) return e;
-            reduce_splits<CT_BF16><<<dim3((unsigned)cdiv(p.n, 256), (unsigned)p.m), 256, 0, s>>>(
-                static_cast<const float *>(pr.ws), splits, p.m * p.n, p.m, p.n, p.c, p.ldc, p.beta, p.bias);
-            return hipGetLastError();
+    if (p.epi.kind != CT_EPI_NONE && !epilogue_fused(pr)) {
+        // The product alone, then the step over it. A SiLU step that keeps the raw product
+        // has the GEMM write it straight to the kept buffer, which the pass then reads.
+        Problem q = pr;
+        EpiParams post = p.epi;
+        q.p.epi.kind = CT_EPI_NONE;
+        void *src = p.c;
+        int64_t ldsrc = p.ldc;
+        if (post.kind == CT_EPI_SILU && post.out0) {
+            src = post.out0;
+            ldsrc = post.ld_out0;
+            q.p.c = post.out0;
+            q.p.ldc = post.ld_out0;
+            q.vec = vec_ok(q);
+            post.out0 = nullptr;
         }
+        const hipError_t e = run(q, s);
+        if (e != hipSuccess) return e;
+        return epilogue_run(post, static_cast<const uint16_t *>(src), ldsrc, static_cast<uint16_t *>(p.c), p.ldc, p.m,
+                            p.n, s);
+    }
+    if (const int splits = mid_split_route(pr); splits > 1) {
+        Problem q = pr;
+        q.splits = splits;
+        q.out = CT_F32;
+        q.tile = TILE_256;
+        q.ws = nullptr;
+        q.ws_bytes = 0;
+        q.p.c = pr.ws;
+        q.p.ldc = p.n;
+        q.p.split_stride = p.m * p.n;
+        q.p.beta = 0;
+        q.p.bias = nullptr;
+        const hipError_t e = run(q, s);
+        if (e != hipSuccess) return e;
+        reduce_splits<CT_BF16><<<dim3((unsigned)cdiv(p.n, 256), (unsigned)p.m), 256, 0, s>>>(
+            static_cast<const float *>(pr.ws), splits, p.m * p.n, p.m, p.n, p.c, p.ldc, p.beta, p.bias);
+        return hipGetLastError();
     }
     if (pr.splits == 1 && pr.out == CT_BF16 && p.m <= 64) {
         // Few rows: the workgroup streams the weight with its 8 waves splitting the reduction.
@@ -1328,7 +1466,7 @@ bool nf4_fusable(const ct_nf4_weight *w) {
 
 using namespace ct;
 
-extern "C" int ct_abi_version(void) { return 8; }
+extern "C" int ct_abi_version(void) { return 10; }
 
 extern "C" const char *ct_status_string(int status) {
     switch (status) {
@@ -1439,6 +1577,67 @@ int take_weight(void *&workspace, int64_t &workspace_bytes, int64_t n, int64_t k
 }  // namespace
 }  // namespace ct
 
+namespace ct {
+namespace {
+// The device view of a caller's epilogue, checked on the host; kind CT_EPI_NONE for null.
+int epilogue_params(const ct_epilogue *e, int64_t n, EpiParams *out) {
+    *out = EpiParams{};
+    if (!e || e->kind == CT_EPI_NONE) return 0;
+    switch (e->kind) {
+        case CT_EPI_RESIDUAL:
+            if (!e->in0) return -CT_EINVAL_POINTER;
+            if (e->ld_in0 < n) return -CT_EINVAL_SHAPE;
+            break;
+        case CT_EPI_SILU:
+            if (!e->in0) return -CT_EINVAL_POINTER;
+            if (e->ld_in0 < n || (e->out0 && e->ld_out0 < n)) return -CT_EINVAL_SHAPE;
+            break;
+        case CT_EPI_DSILU:
+            if (!e->in0 || !e->in1 || !e->out0 || !e->out1) return -CT_EINVAL_POINTER;
+            if (e->ld_in0 < n || e->ld_in1 < n || e->ld_out0 < n || e->ld_out1 < n) return -CT_EINVAL_SHAPE;
+            break;
+        case CT_EPI_ROPE:
+            if (e->head_dim <= 0 || e->head_dim % 2 || n % e->head_dim || e->half < 0 || e->half > e->head_dim / 2 ||
+                n >= (int64_t{1} << 31))
+                return -CT_EINVAL_SHAPE;
+            if (e->half > 0 && (!e->cosine || !e->sine)) return -CT_EINVAL_POINTER;
+            if (e->trig_dtype != CT_F32 && e->trig_dtype != CT_F16 && e->trig_dtype != CT_BF16)
+                return -CT_EINVAL_DTYPE;
+            break;
+        default:
+            return -CT_EINVAL_LAYOUT;
+    }
+    out->kind = e->kind;
+    out->trig_dtype = e->trig_dtype;
+    out->in0 = static_cast<const uint16_t *>(e->in0);
+    out->in1 = static_cast<const uint16_t *>(e->in1);
+    out->ld_in0 = e->ld_in0;
+    out->ld_in1 = e->ld_in1;
+    out->out0 = static_cast<uint16_t *>(e->out0);
+    out->out1 = static_cast<uint16_t *>(e->out1);
+    out->ld_out0 = e->ld_out0;
+    out->ld_out1 = e->ld_out1;
+    out->cosine = e->cosine;
+    out->sine = e->sine;
+    out->head_dim = e->head_dim;
+    out->half = e->half;
+    bool vec = true;
+    const void *side[4] = {e->in0, e->in1, e->out0, e->out1};
+    const int64_t ld[4] = {e->ld_in0, e->ld_in1, e->ld_out0, e->ld_out1};
+    for (int i = 0; i < 4; ++i)
+        if (side[i] && (reinterpret_cast<uintptr_t>(side[i]) % 16 || ld[i] % 8)) vec = false;
+    out->vec = vec;
+    if (e->kind == CT_EPI_ROPE) {
+        const int64_t unit = e->trig_dtype == CT_F32 ? 16 : 8;  // 4 table values
+        out->rope_vec = e->head_dim % 8 == 0 && e->half % 4 == 0 &&
+                        reinterpret_cast<uintptr_t>(e->cosine) % unit == 0 &&
+                        reinterpret_cast<uintptr_t>(e->sine) % unit == 0;
+    }
+    return 0;
+}
+}  // namespace
+}  // namespace ct
+
 extern "C" int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, int64_t r, int32_t nf4) {
     const int64_t inner = ct_gemm_workspace(m, r, k, 0, 1, CT_BF16);
     const int64_t ks[2] = {k, r};
@@ -1451,9 +1650,12 @@ extern "C" int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, 
 extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense, const ct_nf4_weight *w_nf4,
                                  const void *a, const void *b, const void *bias, void *out, int64_t ldo, void *xa,
                                  int64_t ldxa, int32_t xa_given, int64_t m, int64_t n, int64_t k, int64_t r,
-                                 void *workspace, int64_t workspace_bytes, hipStream_t stream) {
+                                 const ct_epilogue *epilogue, void *workspace, int64_t workspace_bytes,
+                                 hipStream_t stream) {
     if (m < 0 || n < 0 || k < 0 || r < 0) return -CT_EINVAL_SHAPE;
     if (m == 0 || n == 0) return 0;
+    EpiParams epi;
+    if (const int st = epilogue_params(epilogue, n, &epi)) return st;
     if (!x || !out || (!w_dense == !w_nf4) || (r > 0 && (!b || !xa || (!xa_given && !a)))) return -CT_EINVAL_POINTER;
     if (ldx < k || ldo < n || (r > 0 && ldxa < r)) return -CT_EINVAL_SHAPE;
     if (w_nf4) {
@@ -1494,6 +1696,7 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
     pr.p.ldc = ldo;
     pr.p.bias = static_cast<const uint16_t *>(bias);
     pr.p.beta = 0;
+    pr.p.epi = epi;
     pr.p.code = w_nf4 ? w_nf4->code : nullptr;
     pr.p.code2 = (w_nf4 && w_nf4->nested) ? w_nf4->code2 : nullptr;
     pr.src[0] = SRC_KC;
@@ -1524,10 +1727,13 @@ extern "C" int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, 
 
 extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_dense, const ct_nf4_weight *w_nf4,
                                  const void *a, const void *b, void *dx, int64_t lddx, void *low, int64_t m,
-                                 int64_t n, int64_t k, int64_t r, int32_t add, void *workspace,
-                                 int64_t workspace_bytes, hipStream_t stream) {
+                                 int64_t n, int64_t k, int64_t r, int32_t add, const ct_epilogue *epilogue,
+                                 void *workspace, int64_t workspace_bytes, hipStream_t stream) {
     if (m < 0 || n < 0 || k < 0 || r < 0) return -CT_EINVAL_SHAPE;
     if (m == 0 || k == 0) return 0;
+    EpiParams epi;
+    if (const int st = epilogue_params(epilogue, k, &epi)) return st;
+    if (epi.kind != CT_EPI_NONE && add) return -CT_EINVAL_LAYOUT;
     if (!dy || !dx || (!w_dense == !w_nf4) || (r > 0 && (!a || !b || !low))) return -CT_EINVAL_POINTER;
     if (lddy < n || lddx < k) return -CT_EINVAL_SHAPE;
     const void *w_trans = nullptr, *a_trans = nullptr;  // w^T [k, n] and a^T [k, r] in the workspace
@@ -1586,6 +1792,7 @@ extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_den
     pr.p.c = dx;
     pr.p.ldc = lddx;
     pr.p.beta = add;
+    pr.p.epi = epi;
     pr.p.code = w_nf4 ? w_nf4->code : nullptr;
     pr.p.code2 = (w_nf4 && w_nf4->nested) ? w_nf4->code2 : nullptr;
     pr.src[0] = SRC_KC;

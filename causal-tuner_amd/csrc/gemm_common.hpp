@@ -3,6 +3,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "epilogue.hpp"
 
 namespace ct {
 
@@ -49,6 +50,8 @@ struct GemmParams {
     // c1[c * ldc1 + i]) instead of next to group 0.
     float *c1;
     int64_t ldc1;
+    // Elementwise step on a bf16 output (kind CT_EPI_NONE: none).
+    EpiParams epi;
 };
 
 // ------------------------------------------------------------------ LDS layout and NF4 decode

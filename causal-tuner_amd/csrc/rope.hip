@@ -10,7 +10,7 @@
 //   e' = T(ec - os), o' = T(oc + es)
 // The inverse rotation negates the sine. HBM-bound elementwise work: one lane per pair.
 
-#include "common.hpp"
+#include "epilogue.hpp"
 
 namespace ct {
 namespace {
@@ -33,10 +33,10 @@ template <int T, int TC, bool INVERSE>
 __device__ __forceinline__ void rotate_pair(const void *x, void *y, int64_t e_index, float c, float s) {
     const float e = load_t<T>(x, e_index), o = load_t<T>(x, e_index + 1);
     if constexpr (INVERSE) s = -s;
-    const float ec = round_to_storage<T>(e * c), os = round_to_storage<T>(o * s);
-    const float oc = round_to_storage<T>(o * c), es = round_to_storage<T>(e * s);
-    store_t<T>(y, e_index, ec - os);
-    store_t<T>(y, e_index + 1, oc + es);
+    float e2, o2;
+    rope_pair<T>(e, o, c, s, e2, o2);
+    store_t<T>(y, e_index, e2);
+    store_t<T>(y, e_index + 1, o2);
 }
 
 // Every pair of x -> y (y may be x): rotated channels rotate, the others are copied.

@@ -53,7 +53,7 @@ int scratch_address(void **out) {
 extern "C" int ct_forward_linear_static(const void *x, int64_t ldx, const void *w_dense, const ct_nf4_weight *w_nf4,
                                         const void *a, const void *b, const void *bias, void *out, int64_t ldo,
                                         void *xa, int64_t ldxa, int32_t xa_given, int64_t m, int64_t n, int64_t k,
-                                        int64_t r, hipStream_t stream) {
+                                        int64_t r, const ct_epilogue *epilogue, hipStream_t stream) {
     if (m < 0 || n < 0 || k < 0 || r < 0) return -CT_EINVAL_SHAPE;
     if (m == 0 || n == 0) return 0;
     const int32_t kind = w_nf4 ? (w_nf4->nested ? 1 : 2) : 0;
@@ -64,6 +64,6 @@ extern "C" int ct_forward_linear_static(const void *x, int64_t ldx, const void *
         const int st = scratch_address(&ws);
         if (st) return st;
     }
-    return ct_forward_linear(x, ldx, w_dense, w_nf4, a, b, bias, out, ldo, xa, ldxa, xa_given, m, n, k, r, ws, need,
-                             stream);
+    return ct_forward_linear(x, ldx, w_dense, w_nf4, a, b, bias, out, ldo, xa, ldxa, xa_given, m, n, k, r, epilogue,
+                             ws, need, stream);
 }

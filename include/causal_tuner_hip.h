@@ -88,6 +88,46 @@ int ct_abi_version(void);
 const char *ct_status_string(int status);
 
 /*
+ * An elementwise step fused into the bf16 output of ct_forward_linear / ct_input_gradient
+ * (or run over it right after the GEMM where a route has no fused epilogue; the values are
+ * the same). y is the projection's output rounded to bf16 as the reference stores it;
+ * tensors are bf16 [m, n] with the given row pitches, indexed like the output.
+ *   CT_EPI_RESIDUAL  out = y + in0                          (the o/down-proj residual,
+ *                    kernels/linear.py:90-91; kernels/mlp_cuda.py:80)
+ *   CT_EPI_SILU      out = bf16(silu(in0)) * y, in0 = gate, y = up; out0 (optional) = y
+ *                    (_activation's forward, kernels/mlp_cuda.py:10-35)
+ *   CT_EPI_DSILU     y = dh; with g = in0, u = in1: out0 = d gate, out1 = d up and
+ *                    out = the hidden activation h (_activation's backward with
+ *                    reconstruction, kernels/mlp_cuda.py:131-133); out0/out1 may be in0/in1
+ *   CT_EPI_ROPE      the partial GPT-J rotation of _owned_qk_rope (kernels/core_cuda.py:
+ *                    133-189): the output is [m, heads, head_dim]; pairs (2c, 2c+1), c < half,
+ *                    rotate by cosine/sine [m, half] of trig_dtype, the rest pass through.
+ * The entry points require add = 0 (no beta) with an epilogue. in0/in1/out0/out1 must not
+ * overlap the main output (the unfused routes store y there before the step reads them).
+ */
+#define CT_EPI_NONE     0
+#define CT_EPI_RESIDUAL 1
+#define CT_EPI_SILU     2
+#define CT_EPI_DSILU    3
+#define CT_EPI_ROPE     4
+typedef struct ct_epilogue {
+    int32_t kind;
+    int32_t trig_dtype;
+    const void *in0;
+    int64_t ld_in0;
+    const void *in1;
+    int64_t ld_in1;
+    void *out0;
+    int64_t ld_out0;
+    void *out1;
+    int64_t ld_out1;
+    const void *cosine;
+    const void *sine;
+    int64_t head_dim;
+    int64_t half;
+} ct_epilogue;
+
+/*
  * Replaces dequantize_nf4 / _decode (kernels/nf4_cuda.py:9-43), the NF4 branch of
  * materialize (kernels/linear.py:6-13).
  * out[e] = out_dtype(storage_dtype(code[nibble(e)] * s[e / blocksize])) for e < rows*cols,
@@ -147,6 +187,18 @@ int ct_gemm(const void *a, int64_t lda, int32_t trans_a,
             const void *b, int64_t ldb, int32_t trans_b,
             void *c, int64_t ldc, int32_t c_dtype, const void *bias, int32_t beta,
             int64_t m, int64_t n, int64_t k, void *workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * The same products for a float32 compute dtype (the reference's torch.mm / addmm with
+ * float32 operands, kernels/linear.py:16-44, TF32 off as in train.py:80-82): float32 a, b,
+ * c and bias, fp32 MFMA products and sums (v_mfma_f32_16x16x4_f32), one in-order reduction
+ * over k per output element (deterministic). Layouts as ct_gemm:
+ *   c[m,n] = sum_k A(m,k) B(k,n) (+ bias[n]) (+ c[m,n] if beta)
+ * With beta = 0, c is only written. No workspace.
+ */
+int ct_gemm_f32(const float *a, int64_t lda, int32_t trans_a, const float *b, int64_t ldb, int32_t trans_b,
+                float *c, int64_t ldc, int32_t beta, const float *bias, int64_t m, int64_t n, int64_t k,
+                hipStream_t stream);
 
 /*
  * 1 when the fused NF4 operand of ct_forward_linear / ct_input_gradient accepts `w`:
@@ -245,7 +297,8 @@ int ct_adamw_step(const ct_adamw_tensor *tensors, int64_t count, const int64_t *
  * rows the reduction may be split across workgroups (fp32 partials in the workspace,
  * added in a fixed order); a weight without double quantization is then decoded first.
  * x [m, k] (ldx), a bf16 [r, k], b bf16 [n, r], bias bf16 [n] or null, out [m, n] (ldo),
- * xa bf16 [m, r] (row pitch ldxa >= r). With xa_given != 0, xa already holds x a^T (a may
+ * xa bf16 [m, r] (row pitch ldxa >= r). `epilogue` (may be null) is an elementwise step on
+ * out (ct_epilogue). With xa_given != 0, xa already holds x a^T (a may
  * be null): projections that share x compute their xa together, x [a_1; a_2; ...]^T in
  * one ct_gemm with ldxa = the summed ranks, and pass column slices. The workspace query
  * takes nf4 = 0 for a bf16 weight, 1 for a double-quantized NF4 weight and 2 for NF4 with
@@ -257,6 +310,7 @@ int ct_forward_linear(const void *x, int64_t ldx,
                       const void *a, const void *b, const void *bias,
                       void *out, int64_t ldo, void *xa, int64_t ldxa, int32_t xa_given,
                       int64_t m, int64_t n, int64_t k, int64_t r,
+                      const ct_epilogue *epilogue,
                       void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
@@ -278,7 +332,8 @@ int ct_forward_linear_static(const void *x, int64_t ldx,
                              const void *w_dense, const ct_nf4_weight *w_nf4,
                              const void *a, const void *b, const void *bias,
                              void *out, int64_t ldo, void *xa, int64_t ldxa, int32_t xa_given,
-                             int64_t m, int64_t n, int64_t k, int64_t r, hipStream_t stream);
+                             int64_t m, int64_t n, int64_t k, int64_t r,
+                             const ct_epilogue *epilogue, hipStream_t stream);
 
 /*
  * Replaces input_gradient (kernels/linear.py:36-39):
@@ -286,8 +341,9 @@ int ct_forward_linear_static(const void *x, int64_t ldx,
  *   dx  = bf16(dy w + low a (+ dx if add))           [m, k]
  * dy [m, n] (lddy), w as in ct_forward_linear (a fused NF4 weight is decoded into LDS in
  * the transposed layout this product needs), a bf16 [r, k], b bf16 [n, r], dx [m, k]
- * (lddx), low bf16 [m, r] contiguous. Workspace query and row regimes as for
- * ct_forward_linear.
+ * (lddx), low bf16 [m, r] contiguous. `epilogue` (may be null, needs add = 0) is an
+ * elementwise step on dx (ct_epilogue: CT_EPI_DSILU for the MLP's down projection).
+ * Workspace query and row regimes as for ct_forward_linear.
  */
 int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, int64_t r, int32_t nf4);
 int ct_input_gradient(const void *dy, int64_t lddy,
@@ -295,6 +351,7 @@ int ct_input_gradient(const void *dy, int64_t lddy,
                       const void *a, const void *b,
                       void *dx, int64_t lddx, void *low,
                       int64_t m, int64_t n, int64_t k, int64_t r, int32_t add,
+                      const ct_epilogue *epilogue,
                       void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*

@@ -14,10 +14,10 @@ from oracle import mlp as omlp
 pytestmark = pytest.mark.gpu
 
 
-def _mlp(h, i, r, *, nf4, tile=None, seed=0, std=.05):
+def _mlp(h, i, r, *, nf4, tile=None, seed=0, std=.05, dtype=torch.bfloat16):
     from causal_tuner.modeling.mlp import MLP
     torch.manual_seed(seed)
-    module = MLP(h, i, rank=r, device="cuda", tile=tile)
+    module = MLP(h, i, rank=r, base_dtype=dtype, compute_dtype=dtype, device="cuda", tile=tile)
     for projection in (module.gate_proj, module.up_proj, module.down_proj):
         torch.nn.init.normal_(projection.lora_B, std=std)
         if nf4:
@@ -83,12 +83,14 @@ def test_fused_mlp_saves_only_boundary_and_weights(nf4, monkeypatch):
     output.sum().backward()
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("tile", [0, 5])
 @pytest.mark.parametrize("nf4", [False, True])
-def test_saved_mlp_matches_recompute_and_preserves_repeated_backward(tile, nf4, monkeypatch):
+def test_saved_mlp_matches_recompute_and_preserves_repeated_backward(tile, nf4, dtype, monkeypatch):
+    """tests/test_mlp_cache.py:15-49 (float32 and bf16; plus NF4 bases)."""
     from causal_tuner.kernels import mlp_cuda
-    module = _mlp(32, 68, 4, nf4=nf4, tile=tile)
-    x = torch.randn(2, 7, 32, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    module = _mlp(32, 68, 4, nf4=nf4, tile=tile, dtype=dtype)
+    x = torch.randn(2, 7, 32, device="cuda", dtype=dtype, requires_grad=True)
     original = x.detach().clone()
     signal = torch.randn_like(x)
     params = _params(module, x)
@@ -106,6 +108,7 @@ def test_saved_mlp_matches_recompute_and_preserves_repeated_backward(tile, nf4, 
     def forbidden(*a, **kw):
         raise AssertionError("Cached backward must not recompute gate/up projections")
     monkeypatch.setattr(mlp_cuda, "forward_linear", forbidden)
+    monkeypatch.setattr(mlp_cuda._MLPProjections, "gate_up", forbidden)
     gradients = torch.autograd.grad(actual, params, signal, retain_graph=True)
     repeated = torch.autograd.grad(actual, params, signal)
     torch.testing.assert_close(actual, expected, rtol=0, atol=0)
@@ -116,6 +119,57 @@ def test_saved_mlp_matches_recompute_and_preserves_repeated_backward(tile, nf4, 
     for value, snapshot in zip(retained, snapshots):
         torch.testing.assert_close(value, snapshot, rtol=0, atol=0)
     torch.testing.assert_close(x, original, rtol=0, atol=0)
+
+
+def _plain_linear(module, x):
+    """tests/test_fast_training.py:18-23: the projection as plain torch ops."""
+    dtype = module.compute_dtype
+    x = x.to(dtype)
+    weight = module.base_weight().to(dtype)
+    bias = None if module.bias is None else module.bias.to(dtype)
+    return F.linear(x, weight, bias) + F.linear(F.linear(x, module.lora_A.to(dtype)), module.lora_B.to(dtype))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("train_input", [False, True])
+@pytest.mark.parametrize("mixed_ranks", [False, True])
+@pytest.mark.parametrize("cache", [False, True])
+def test_fused_tiled_mlp_independent_gradients(dtype, train_input, mixed_ranks, cache):
+    """tests/test_fast_training.py:26-57 with its tolerances (float32: rtol 3e-5, atol 2e-6
+    against torch's float32 products with TF32 off): the tiny config's MLP (32 -> 68,
+    rank 4, tile 5), mixed ranks 3/5/7, cache on and off."""
+    import copy
+    from causal_tuner.modeling.lora import Projection
+    from causal_tuner.modeling.mlp import MLP
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.manual_seed(4)
+    module = MLP(32, 68, rank=4, base_dtype=dtype, compute_dtype=dtype, device="cuda", tile=5)
+    module.cache_intermediates = cache
+    if mixed_ranks:
+        for name, rank in (("gate_proj", 3), ("up_proj", 5), ("down_proj", 7)):
+            original = getattr(module, name)
+            setattr(module, name, Projection(original.weight.shape[1], original.weight.shape[0], rank=rank,
+                                             base_dtype=dtype, compute_dtype=dtype, device="cuda"))
+    for name, parameter in module.named_parameters():
+        if "lora_B" in name:
+            torch.nn.init.normal_(parameter, std=.1)
+    reference = copy.deepcopy(module)
+    x = torch.randn(2, 7, 32, device="cuda", dtype=dtype, requires_grad=train_input)
+    y = x.detach().clone().requires_grad_(train_input)
+    actual = module(x)
+    expected = _plain_linear(reference.down_proj, F.silu(_plain_linear(reference.gate_proj, y)) *
+                             _plain_linear(reference.up_proj, y))
+    tolerance = dict(rtol=.04, atol=.003) if dtype == torch.bfloat16 else dict(rtol=3e-5, atol=2e-6)
+    torch.testing.assert_close(actual, expected, **tolerance)
+    signal = torch.randn_like(actual)
+    actual.backward(signal)
+    expected.backward(signal)
+    if train_input:
+        torch.testing.assert_close(x.grad, y.grad, **tolerance)
+    for (name, a), (_, b) in zip(module.named_parameters(), reference.named_parameters()):
+        if a.requires_grad:
+            assert a.grad.dtype == torch.float32, name
+            torch.testing.assert_close(a.grad, b.grad, **tolerance)
 
 
 def test_nf4_fused_tiled_mlp_gradients():

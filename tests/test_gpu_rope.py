@@ -99,25 +99,28 @@ def _group(width, head_dim, dtype=torch.bfloat16, nf4=False, seed=0):
     return modules
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("tile", [0, 5])
 @pytest.mark.parametrize("head_dim,rotary_dim", [(8, 4), (128, 64)])
-def test_projection_owned_rotary_preserves_shared_gradients(tile, head_dim, rotary_dim, monkeypatch):
-    """tests/test_kernel_workspaces.py:17-63 (bf16)."""
+def test_projection_owned_rotary_preserves_shared_gradients(dtype, tile, head_dim, rotary_dim, monkeypatch):
+    """tests/test_kernel_workspaces.py:17-63 with its tolerances: bit-exact in bf16,
+    2e-6 in float32 (the float32 products run on ct_gemm_f32)."""
     import causal_tuner.kernels.core_cuda as core
     from causal_tuner.kernels.linear import project_group
     from causal_tuner.modeling.rotary import rotate
     width = head_dim * 4
-    modules = _group(width, head_dim)
-    x = torch.randn(2, 7, width, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    modules = _group(width, head_dim, dtype)
+    x = torch.randn(2, 7, width, device="cuda", dtype=dtype, requires_grad=True)
     original_input = x.detach().clone()
     angles = torch.arange(14, device="cuda").reshape(2, 7, 1) * 60000 * torch.rand(rotary_dim // 2, device="cuda")
-    cosine, sine = angles.cos().to(torch.bfloat16), angles.sin().to(torch.bfloat16)
+    cosine, sine = angles.cos().to(dtype), angles.sin().to(dtype)
     actual = project_group(modules, x, tile, rotary=(cosine, sine, head_dim))
     raw = project_group(modules, x, tile)
     expected = tuple(rotate(t.reshape(2, 7, -1, head_dim), cosine, sine).reshape_as(t) if i < 2 else t
                      for i, t in enumerate(raw))
+    tolerance = dict(rtol=0, atol=0) if dtype == torch.bfloat16 else dict(rtol=2e-6, atol=2e-6)
     for a, e in zip(actual, expected):
-        assert torch.equal(a, e)
+        torch.testing.assert_close(a, e, **tolerance)
     for a, r in zip(actual[:2], raw[:2]):
         assert torch.equal(a.reshape(2, 7, -1, head_dim)[..., rotary_dim:],
                            r.reshape(2, 7, -1, head_dim)[..., rotary_dim:])
@@ -138,7 +141,7 @@ def test_projection_owned_rotary_preserves_shared_gradients(tile, head_dim, rota
     repeated = torch.autograd.grad(actual, parameters, signals)
     assert 0 < largest_tile <= (tile or 4096)
     for a, e, r in zip(ag, eg, repeated):
-        assert torch.equal(a, e)
+        torch.testing.assert_close(a, e, **tolerance)
         assert torch.equal(a, r)
     assert torch.equal(shared, saved_signal)
     assert torch.equal(x, original_input)

@@ -36,11 +36,11 @@ def _run(entry, problem, m, k, n, r):
               out.data_ptr(), n, xa.data_ptr(), r, 0, m, n, k, r)
     stream = _native.stream_of(x)
     if entry == "static":
-        status = lib.ct_forward_linear_static(*common, stream)
+        status = lib.ct_forward_linear_static(*common, None, stream)
     else:
         need = lib.ct_forward_linear_workspace(m, n, k, r, 1)
         ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
-        status = lib.ct_forward_linear(*common, ws.data_ptr(), ws.numel(), stream)
+        status = lib.ct_forward_linear(*common, None, ws.data_ptr(), ws.numel(), stream)
     assert status == 0, (entry, status)
     return out, xa
 
@@ -66,5 +66,5 @@ def test_static_scratch_refuses_problems_beyond_its_maximum():
     desc = _native.NF4Weight(packed=256, absmax=256, code=256, code2=256, absmax2=256, offset=256, rows=n, cols=k,
                              blocksize=64, blocksize2=256, nested=1, storage_dtype=_native.CT_BF16)
     status = lib.ct_forward_linear_static(16, k, None, ctypes.byref(desc), 16, 16, None, 16, n, 16, r, 0, m, n, k, r,
-                                          None)
+                                          None, None)
     assert status == -5
