@@ -197,8 +197,43 @@ def epilogue(kind, rows, in0=None, in1=None, out0=None, out1=None, rotary=None):
     return e
 
 
+def _nf4_key(weight, state):
+    nested = bool(state.nested)
+    aux = state.state2 if nested else None
+    return (weight.data_ptr(), state.absmax.data_ptr(), state.code.data_ptr(), tuple(state.shape),
+            int(state.blocksize), state.dtype, nested,
+            (aux.code.data_ptr(), aux.absmax.data_ptr(), state.offset.data_ptr(), int(aux.blocksize)) if nested
+            else None)
+
+
 def nf4_descriptor(weight, state):
-    """Build the ct_nf4_weight view of a packed weight and its QuantState (no copies)."""
+    """The ct_nf4_weight view of a packed weight and its QuantState (no copies). Kept on the
+    state with the addresses it was built from, and rebuilt when any of them changes."""
+    key = _nf4_key(weight, state)
+    cached = getattr(state, "_ct_descriptor", None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    desc = _build_nf4_descriptor(weight, state)
+    try:
+        state._ct_descriptor = (key, desc, None)
+    except AttributeError:   # a state type without attribute storage: no cache
+        pass
+    return desc
+
+
+def nf4_fused_supported(weight, state):
+    """ct_nf4_fused_supported of the weight's descriptor, kept beside the descriptor."""
+    desc = nf4_descriptor(weight, state)
+    cached = getattr(state, "_ct_descriptor", None)
+    if cached is not None and cached[1] is desc and cached[2] is not None:
+        return cached[2]
+    supported = library().ct_nf4_fused_supported(desc) == 1
+    if cached is not None and cached[1] is desc:
+        state._ct_descriptor = (cached[0], desc, supported)
+    return supported
+
+
+def _build_nf4_descriptor(weight, state):
     nested = bool(state.nested)
     aux = state.state2 if nested else None
     numel = 1

@@ -23,6 +23,7 @@ except in `accumulate`, which keeps the reference's addmm for operands that are 
 import contextlib
 import contextvars
 import ctypes
+import functools
 
 import torch
 
@@ -78,6 +79,12 @@ def fusable(*tensors):
     return all(t.is_cuda and t.dtype == torch.bfloat16 and t.dim() == 2 and t.stride(1) == 1
                and t.stride(0) >= t.shape[1] and t.stride(0) % 8 == 0 and _aligned(t)
                for t in tensors if t is not None)
+
+
+@functools.lru_cache(maxsize=4096)
+def _query(name, *args):
+    """A workspace-size query of the library (pure in its integer arguments), cached."""
+    return getattr(_native.library(), name)(*args)
 
 
 def _workspace(nbytes, device):
@@ -156,7 +163,7 @@ def _mm_bf16(left, right, out, *, add=False):
     if add and target.buffer is not out:
         target.buffer.copy_(out)
     lib = _native.library()
-    ws = _workspace(lib.ct_gemm_workspace(m, n, k, tl, tr, _native.CT_BF16), out.device)
+    ws = _workspace(_query("ct_gemm_workspace", m, n, k, tl, tr, _native.CT_BF16), out.device)
     with _native.device_of(out):
         status = lib.ct_gemm(_native.ptr(lt), ldl, tl, _native.ptr(rt), ldr, tr, _native.ptr(target.buffer),
                              target.ld, _native.CT_BF16, None, int(add), m, n, k, _native.ptr(ws), ws.numel(),
@@ -243,7 +250,7 @@ def accumulate(output, left, right, *, add=True):
         lt, ldl, tl = _operand(left)
         rt, ldr, tr = _operand(right)
         lib = _native.library()
-        ws = _workspace(lib.ct_accumulate_workspace(p, q, j), output.device)
+        ws = _workspace(_query("ct_accumulate_workspace", p, q, j), output.device)
         with _native.device_of(output):
             status = lib.ct_accumulate(_native.ptr(target.buffer), target.ld, _native.ptr(lt), ldl, tl,
                                        _native.ptr(rt), ldr, tr, p, q, j, int(add) if target.buffer is output else
@@ -304,7 +311,7 @@ def _forward(x, weight, state, a, b, bias, out, xa, xa_given=False, epilogue=Non
         low.buffer.copy_(xa)
     desc = None if state is None else _native.nf4_descriptor(w, state)
     lib = _native.library()
-    ws = _workspace(lib.ct_forward_linear_workspace(m, n, k, r, _native.nf4_kind(desc)), x.device)
+    ws = _workspace(_query("ct_forward_linear_workspace", m, n, k, r, _native.nf4_kind(desc)), x.device)
     with _native.device_of(x):
         status = lib.ct_forward_linear(
             _native.ptr(x), ldx, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),
@@ -350,7 +357,7 @@ def _input_gradient(dy, weight, state, a, b, dx, low, add, epilogue=None):
         target.buffer.copy_(dx)
     desc = None if state is None else _native.nf4_descriptor(w, state)
     lib = _native.library()
-    ws = _workspace(lib.ct_input_gradient_workspace(m, n, k, r, _native.nf4_kind(desc)), dy.device)
+    ws = _workspace(_query("ct_input_gradient_workspace", m, n, k, r, _native.nf4_kind(desc)), dy.device)
     with _native.device_of(dy):
         status = lib.ct_input_gradient(
             _native.ptr(dy), lddy, None if desc is not None else _native.ptr(w), desc, _native.ptr(a),
@@ -381,7 +388,7 @@ def parameter_gradients(x, dy, da, db, low, xa, *, add):
         accumulate(db, dy.T, xa, add=add)
         return
     lib = _native.library()
-    ws = _workspace(lib.ct_parameter_gradients_workspace(m, n, k, r), x.device)
+    ws = _workspace(_query("ct_parameter_gradients_workspace", m, n, k, r), x.device)
     with _native.device_of(x):
         status = lib.ct_parameter_gradients(_native.ptr(x), ldx, _native.ptr(dy), lddy, _native.ptr(low), ldlow,
                                              _native.ptr(xa), ldxa, _native.ptr(da), _native.ptr(db), m, n, k, r,
@@ -415,8 +422,7 @@ class _Base:
         self.weight, self.state, self.matrix = weight, None, None
         if state is not None and weight.is_cuda and dtype == torch.bfloat16 and weight.dtype == torch.uint8 \
                 and weight.is_contiguous() and state.quant_type == "nf4":
-            desc = _native.nf4_descriptor(weight, state)
-            if _native.library().ct_nf4_fused_supported(desc) == 1:
+            if _native.nf4_fused_supported(weight, state):
                 self.state = state
         if self.state is None:
             self.matrix = materialize(weight, state, dtype)
@@ -454,7 +460,9 @@ def projection_budget(nbytes):
     """Let projection groups called without a tile inside this block spend up to `nbytes`
     of device memory on row-proportional state: when a group's whole input fits, it runs
     all rows as one tile and keeps each projection's forward xa = x a^T for its backward
-    instead of recomputing it. The default budget is 0: 4096-row tiles and nothing saved
+    instead of recomputing it, and with it the compute-dtype LoRA factors (a fixed
+    rank x (in + out) elements per projection) instead of casting them again. The default
+    budget is 0: 4096-row tiles and nothing saved
     but the input and the parameters, as in the reference (linear.py:59-130). The budget
     is read when the forward runs; the backward follows the forward's choice."""
     if nbytes < 0:
@@ -542,7 +550,9 @@ class _LoRAGroup(torch.autograd.Function):
                     epilogue = _native.epilogue(_native.CT_EPI_RESIDUAL, len(part), in0=residual_flat[window])
                 base.forward(part, factors[2*index], factors[2*index+1], biases[index], outputs[index][window],
                              columns[index][rows], xa_given=stack is not None, epilogue=epilogue)
-        kept = columns if keep else []
+        # Under a projection budget the backward also reuses the compute-dtype factors
+        # (the reference casts them again, linear.py:108: the same values).
+        kept = [*columns, *factors] if keep else []
         ctx.kept = len(kept)
         ctx.save_for_backward(x, cosine, sine, *parameters, *kept)
         del factors, stack, bases, xa, columns, kept
@@ -558,13 +568,17 @@ class _LoRAGroup(torch.autograd.Function):
     def backward(ctx, *grad_outputs):
         x, cosine, sine, *rest = ctx.saved_tensors
         count = len(ctx.states)
-        parameters, kept = rest[:4*count], rest[4*count:]
+        parameters, kept = rest[:4*count], rest[4*count:4*count+count]
+        saved_factors = rest[4*count+count:]
         flat = x.reshape(-1, x.shape[-1]).to(ctx.dtype)
         dx = torch.empty_like(flat) if ctx.needs_input_grad[0] else None
         if ctx.head_dim:
             cosine, sine = (value.reshape(-1, value.shape[-1]) for value in (cosine, sine))
         step, span = ctx.step, min(ctx.step, len(flat))
-        factors, stack = group_factors(parameters, count, ctx.dtype, x)
+        if saved_factors:
+            factors, stack = list(saved_factors), None
+        else:
+            factors, stack = group_factors(parameters, count, ctx.dtype, x)
         bases = [_Base(parameters[4*i], state, ctx.dtype) if dx is not None else None
                  for i, state in enumerate(ctx.states)]
         ranks = [len(parameters[4*i+1]) for i in range(count)]
@@ -625,7 +639,7 @@ def _low_rank(x, factor, out, *, transpose):
     factor = factor.contiguous()
     target = _Output(out)
     lib = _native.library()
-    ws = _workspace(lib.ct_gemm_workspace(m, r, k, 0, int(transpose), _native.CT_BF16), x.device)
+    ws = _workspace(_query("ct_gemm_workspace", m, r, k, 0, int(transpose), _native.CT_BF16), x.device)
     with _native.device_of(x):
         status = lib.ct_gemm(_native.ptr(x), ldx, 0, _native.ptr(factor), k if transpose else r, int(transpose),
                              _native.ptr(target.buffer), target.ld, _native.CT_BF16, None, 0, m, r, k,

@@ -40,13 +40,26 @@ __global__ __launch_bounds__(kCastThreads) void cast_f32_bf16(const CastTable t)
         const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0 &&
                          (e & 7) == 0;
         if (vec) {
+            // at most kSpan / (8 * kCastThreads) = 4 groups per lane: every load is issued
+            // before the first store, so the lane waits on memory once
+            constexpr int kGroups = kSpan / (8 * kCastThreads);
             const int64_t full = e + ((end - e) & ~int64_t{7});
-            for (int64_t j = e + 8 * (int64_t)threadIdx.x; j < full; j += 8 * kCastThreads) {
-                const float4 a = *reinterpret_cast<const float4 *>(src + j);
-                const float4 b = *reinterpret_cast<const float4 *>(src + j + 4);
-                *reinterpret_cast<uint4 *>(dst + j) =
-                    make_uint4(pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w), pack_bf16x2(b.x, b.y),
-                               pack_bf16x2(b.z, b.w));
+            float4 a[kGroups], b[kGroups];
+#pragma unroll
+            for (int u = 0; u < kGroups; ++u) {
+                const int64_t j = e + 8 * ((int64_t)threadIdx.x + (int64_t)u * kCastThreads);
+                if (j < full) {
+                    a[u] = *reinterpret_cast<const float4 *>(src + j);
+                    b[u] = *reinterpret_cast<const float4 *>(src + j + 4);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kGroups; ++u) {
+                const int64_t j = e + 8 * ((int64_t)threadIdx.x + (int64_t)u * kCastThreads);
+                if (j < full)
+                    *reinterpret_cast<uint4 *>(dst + j) =
+                        make_uint4(pack_bf16x2(a[u].x, a[u].y), pack_bf16x2(a[u].z, a[u].w),
+                                   pack_bf16x2(b[u].x, b[u].y), pack_bf16x2(b[u].z, b[u].w));
             }
             e = full;
         }

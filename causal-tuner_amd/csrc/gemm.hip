@@ -1855,6 +1855,19 @@ struct ParamPlan {
 ParamPlan param_plan(int64_t m, int64_t n, int64_t k, int64_t r) {
     ParamPlan pl{};
     pl.tile = r > 128 ? TILE_256 : (r > 64 ? TILE_128 : TILE_64);
+    if (pl.tile != TILE_64 && m <= 2048) {
+        // Few tokens: the reduction is short and writing the fp32 outputs dominates, so
+        // smaller tiles spread them over more workgroups (two per CU at 128 x 128) and no
+        // split partials are written (measured at 16-1024 tokens: 36 -> 21 us at C5's
+        // 6144 x 24576, 33 -> 8.4 us at C1's 1024 x 1024, rank 256).
+        const int64_t tiles128 = cdiv(r, 128) * (cdiv(k, 128) + cdiv(n, 128));
+        pl.tile = tiles128 >= 128 ? TILE_128 : TILE_64;
+        const int64_t e = kTileEdge[pl.tile];
+        pl.gt = (int)cdiv(k, e);
+        pl.width = pl.gt * e + n;
+        pl.splits = 1;
+        return pl;
+    }
     const int64_t e = kTileEdge[pl.tile];
     pl.gt = (int)cdiv(k, e);
     pl.width = pl.gt * e + n;
