@@ -8,19 +8,35 @@
 namespace ct {
 namespace {
 
-// One lane per 8 consecutive columns of one row (the last group of a row may be shorter);
-// `vec`: src and dst are 16-byte aligned with pitches of a multiple of 8.
+// One lane per 8 consecutive columns of a row (the last group of a row may be shorter):
+// grid.x covers a row's column groups, grid.y strides over the rows (no index division).
+// One instance per kind and access width keeps each kernel's registers to its own step.
+// VEC: src and dst are 16-byte aligned with pitches of a multiple of 8.
+template <int KIND, bool VEC>
 __global__ __launch_bounds__(256) void epilogue_rows(const EpiParams e, const uint16_t *src, int64_t ldsrc,
-                                                     uint16_t *dst, int64_t lddst, int64_t m, int64_t n, int vec) {
-    const int64_t groups = (n + 7) / 8;
-    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (g >= groups * m) return;
-    const int64_t row = g / groups, col = (g % groups) * 8;
+                                                     uint16_t *dst, int64_t lddst, int64_t m, int64_t n) {
+    const int64_t col = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (col >= n) return;
     const int count = n - col < 8 ? (int)(n - col) : 8;
-    float y[8];
-    load_bf16_run<8>(src + row * ldsrc + col, count, vec, y);
-    epilogue_values<8>(e, row, col, count, y);
-    store_bf16_run<8>(dst + row * lddst + col, count, vec, y);
+    for (int64_t row = blockIdx.y; row < m; row += gridDim.y) {
+        float y[8];
+        EpiSide<8> side;
+        load_bf16_run<8>(src + row * ldsrc + col, count, VEC, y);
+        epilogue_load<KIND, 8>(e, row, col, count, side);
+        epilogue_apply<KIND, 8>(e, row, col, count, side, y);
+        store_bf16_run<8>(dst + row * lddst + col, count, VEC, y);
+    }
+}
+
+template <int KIND>
+hipError_t launch_rows(const EpiParams &e, const uint16_t *src, int64_t ldsrc, uint16_t *dst, int64_t lddst, int64_t m,
+                       int64_t n, bool vec, hipStream_t stream) {
+    const int64_t groups = (n + 7) / 8;
+    if (cdiv(groups, 256) > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)cdiv(groups, 256), (unsigned)(m < 65535 ? m : 65535));
+    if (vec) epilogue_rows<KIND, true><<<grid, dim3(256), 0, stream>>>(e, src, ldsrc, dst, lddst, m, n);
+    else epilogue_rows<KIND, false><<<grid, dim3(256), 0, stream>>>(e, src, ldsrc, dst, lddst, m, n);
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -28,11 +44,15 @@ __global__ __launch_bounds__(256) void epilogue_rows(const EpiParams e, const ui
 hipError_t epilogue_run(const EpiParams &e, const uint16_t *src, int64_t ldsrc, uint16_t *dst, int64_t lddst, int64_t m,
                         int64_t n, hipStream_t stream) {
     if (e.kind == CT_EPI_NONE || m <= 0 || n <= 0) return hipSuccess;
-    const int64_t lanes = m * ((n + 7) / 8);
-    const int vec = reinterpret_cast<uintptr_t>(src) % 16 == 0 && ldsrc % 8 == 0 &&
-                    reinterpret_cast<uintptr_t>(dst) % 16 == 0 && lddst % 8 == 0;
-    epilogue_rows<<<dim3((unsigned)cdiv(lanes, 256)), dim3(256), 0, stream>>>(e, src, ldsrc, dst, lddst, m, n, vec);
-    return hipGetLastError();
+    const bool vec = reinterpret_cast<uintptr_t>(src) % 16 == 0 && ldsrc % 8 == 0 &&
+                     reinterpret_cast<uintptr_t>(dst) % 16 == 0 && lddst % 8 == 0;
+    switch (e.kind) {
+        case CT_EPI_RESIDUAL: return launch_rows<CT_EPI_RESIDUAL>(e, src, ldsrc, dst, lddst, m, n, vec, stream);
+        case CT_EPI_SILU: return launch_rows<CT_EPI_SILU>(e, src, ldsrc, dst, lddst, m, n, vec, stream);
+        case CT_EPI_DSILU: return launch_rows<CT_EPI_DSILU>(e, src, ldsrc, dst, lddst, m, n, vec, stream);
+        case CT_EPI_ROPE: return launch_rows<CT_EPI_ROPE>(e, src, ldsrc, dst, lddst, m, n, vec, stream);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace ct
