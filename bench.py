@@ -21,6 +21,9 @@ projections  C1 and C5: one projection fwd+bwd at several row counts, with the b
           applies (HBM for few rows, bf16 MFMA for many).
 skinny    C5 at 16 and 64 rows: the few-row forward and dx GEMM kernels alone, GB/s of their
           algorithmic bytes against the HBM peak (--skinny-only runs just this leg).
+epilogues the projection epilogues at C4 shapes (RoPE, residual, SiLU x up, SiLU backward):
+          a call with its step in the library against the call without it plus the
+          separate kernel (--epilogue-only runs just this leg).
 c4        C4: tokens/s of a full LoRA training step of the 24-layer decoder on 4096 packed
           tokens (modeling/decoder.py, FusedAdamW; --c4-only runs just this leg).
 cpu_baseline  the reference's op sequence on the host CPU (oracle/lora.py), bounded sample.
@@ -454,6 +457,93 @@ def skinny_measure(device, shapes=((6144, 24576), (24576, 6144)), rows_list=(16,
     return results
 
 
+def _events_us(fn, reps):
+    """GPU time per call of `fn` in microseconds: HIP events around `reps` calls queued
+    behind a spin kernel, so host-side launch cost does not show."""
+    fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(2e8))
+    start.record()
+    for _ in range(reps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) * 1e3 / reps
+
+
+def epilogue_measure(device, rows=4096, reps=20, rank=R):
+    """The projection epilogues at C4's shapes (4096 rows, NF4 bases, rank 256): each
+    projection call with its elementwise step in the library (fused into the GEMM or, where
+    that measured slower, a pass right after it), against the same call without the step
+    followed by the separate kernel the callers ran before (ct_rope, torch's add_,
+    ct_silu_multiply). Both sides compute the same bits."""
+    from causal_tuner.kernels import _native
+    from causal_tuner.kernels.core_cuda import _rope
+    from causal_tuner.kernels.linear import _Base, _forward, _input_gradient
+    from causal_tuner.kernels.mlp_cuda import _silu_kernel
+    from causal_tuner.quant.nf4 import quantize_nf4
+    g = torch.Generator(device=device).manual_seed(11)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, device=device, generator=g) * scale).to(torch.bfloat16)
+
+    def base(k, n):
+        packed, state = quantize_nf4((torch.randn(n, k, device=device, generator=g) * 0.02).to(torch.bfloat16))
+        return _Base(packed, state, torch.bfloat16), rnd(rank, k, scale=0.02), rnd(n, rank, scale=0.01)
+
+    results = {}
+    m = rows
+    # q with RoPE (2048 -> 2048, heads of 128, 64 rotated channels); o and down with the
+    # residual (2048 -> 2048, 8192 -> 2048); up with SiLU x gate keeping up (2048 -> 8192);
+    # dh with the SiLU backward (dy 2048 wide -> dh 8192 wide).
+    for name, k, n, kind in (("q_rope", 2048, 2048, "rope"), ("o_residual", 2048, 2048, "residual"),
+                             ("down_residual", 8192, 2048, "residual"), ("up_silu_keep", 2048, 8192, "silu"),
+                             ("dh_silu_backward", 8192, 2048, "dsilu")):
+        bs, a, b = base(k, n)
+        weight = bs.matrix if bs.state is None else bs.weight
+        if kind == "dsilu":
+            dy, gate, up = rnd(m, n), rnd(m, k, scale=3.0), rnd(m, k)
+            out, low = torch.empty(m, k, device=device, dtype=torch.bfloat16), torch.empty(m, rank, device=device,
+                                                                                          dtype=torch.bfloat16)
+            dg, du = torch.empty_like(gate), torch.empty_like(up)
+            epi = _native.epilogue(_native.CT_EPI_DSILU, m, in0=gate, in1=up, out0=dg, out1=du)
+            plain = lambda: _input_gradient(dy, weight, bs.state, a, b, out, low, False)
+            fused = lambda: _input_gradient(dy, weight, bs.state, a, b, out, low, False, epi)
+            separate = lambda: _silu_kernel(gate, up, out, dg, du, backward=True, reconstruct=True)
+        else:
+            x = rnd(m, k)
+            out, xa = torch.empty(m, n, device=device, dtype=torch.bfloat16), torch.empty(m, rank, device=device,
+                                                                                          dtype=torch.bfloat16)
+            if kind == "rope":
+                angle = torch.rand(m, 32, device=device, generator=g) * 1e4
+                cosine, sine = angle.cos().to(torch.bfloat16), angle.sin().to(torch.bfloat16)
+                epi = _native.epilogue(_native.CT_EPI_ROPE, m, rotary=(cosine, sine, 128))
+                separate = lambda: _rope(out, out, cosine, sine, 128, inverse=False, rotated_only=True)
+            elif kind == "residual":
+                residual = rnd(m, n)
+                epi = _native.epilogue(_native.CT_EPI_RESIDUAL, m, in0=residual)
+                separate = lambda: out.add_(residual)
+            else:
+                gate, kept = rnd(m, n, scale=3.0), torch.empty(m, n, device=device, dtype=torch.bfloat16)
+                epi = _native.epilogue(_native.CT_EPI_SILU, m, in0=gate, out0=kept)
+                separate = lambda: _silu_kernel(gate, kept, out, None, None, backward=False, reconstruct=True)
+            plain = lambda: _forward(x, weight, bs.state, a, b, None, out, xa)
+            fused = lambda: _forward(x, weight, bs.state, a, b, None, out, xa, False, epi)
+        def both():
+            plain()
+            separate()
+        t_plain, t_fused, t_both = (_events_us(fn, reps) for fn in (plain, fused, both))
+        results[name] = {"rows": m, "in": k, "out": n, "call_us": round(t_plain, 1),
+                         "with_step_us": round(t_fused, 1), "call_then_separate_us": round(t_both, 1),
+                         "saved_us": round(t_both - t_fused, 1)}
+        log(f"  {name:17s} call {t_plain:7.1f} us | with its step {t_fused:7.1f} us | "
+            f"call + separate kernel {t_both:7.1f} us")
+        del bs, a, b, out
+    torch.cuda.empty_cache()
+    return results
+
+
 # The reference's runtime option mlp_cache_budget_bytes (training/execution.py:65-66):
 # the C4 step keeps every layer's gate/up outputs and xa (138 MB per layer at 4096 tokens,
 # 3.3 GB for 24), which MI355X's 288 GB holds; the reference's own policy enables the same
@@ -539,6 +629,8 @@ def main():
                         help="run only the C2 standalone dequant leg and print its JSON")
     parser.add_argument("--skinny-only", action="store_true",
                         help="run only the C5 few-row kernel leg and print its JSON")
+    parser.add_argument("--epilogue-only", action="store_true",
+                        help="run only the projection-epilogue leg (C4 shapes) and print its JSON")
     parser.add_argument("--no-c4", action="store_true", help="skip the C4 training-step leg")
     parser.add_argument("--c4-only", action="store_true", help="run only the C4 training-step leg")
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MiB",
@@ -564,6 +656,9 @@ def main():
         return
     if args.c4_only:
         print(json.dumps({"c4": c4_measure(device)}), flush=True)
+        return
+    if args.epilogue_only:
+        print(json.dumps({"epilogues": epilogue_measure(device)}), flush=True)
         return
 
     log("building C3 layer (NF4 quantization of seven projections)...")
@@ -635,6 +730,10 @@ def main():
     if not args.no_sweep:
         log("C5 few-row kernels (M 16 and 64, weights rotated past the Infinity Cache):")
         skinny = skinny_measure(device)
+    epilogues = None
+    if not args.no_sweep:
+        log("projection epilogues at C4 shapes (4096 rows):")
+        epilogues = epilogue_measure(device)
     c4 = None
     if not args.no_c4:
         log("C4 training step (24 layers, 4096 tokens):")
@@ -667,6 +766,9 @@ def main():
         "skinny": {"workload": "C5 M 16 and 64: the forward and dx GEMM kernels alone on the packed NF4 weight "
                                "(split reduction included), four weight copies in rotation",
                    "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "results": skinny},
+        "epilogues": {"workload": "C4 shapes, 4096 rows: a projection call with its elementwise step in the "
+                                  "library against the call without it plus the separate kernel",
+                      "results": epilogues},
         "c4": c4,
     }
     print(json.dumps(line), flush=True)
