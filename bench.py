@@ -185,9 +185,11 @@ def skinny_bytes(m, k, n, r):
 
 def projection_measure(device, shapes, rows_list, iters=20, rank=R):
     """One NF4-LoRA projection fwd+bwd through project_group + autograd (the reference's
-    operator path), per shape and row count: average ms over `iters` steps (HIP events),
-    algorithmic TFLOP/s and GB/s, and the fraction of the bound that applies (HBM for
-    few rows, bf16 MFMA for many). Under the C3 step's projection budget, as there."""
+    operator path), per shape and row count: average ms over `iters` back-to-back steps
+    (HIP events; the rates use it), the GPU's own time per step (the steps queued behind
+    a spin kernel, so host-side work is hidden), algorithmic TFLOP/s and GB/s, and the
+    fraction of the bound that applies (HBM for few rows, bf16 MFMA for many). Under the
+    C3 step's projection budget, as there."""
     from causal_tuner.kernels.linear import project_group, projection_budget
     from causal_tuner.modeling.lora import Projection
     results = {}
@@ -206,14 +208,17 @@ def projection_measure(device, shapes, rows_list, iters=20, rank=R):
                     out, = project_group((module,), x)
                 torch.autograd.grad(out, (x, module.lora_A, module.lora_B), dy)
             ms = time_events(step, iters)
+            # the same steps queued behind a spin kernel: the GPU's own time per step, which
+            # the host-side operator path (autograd, ctypes calls) hides at few rows
+            gpu_ms = _events_us(step, iters) * 1e-3
             flops, nbytes = projection_flops(m, k, n, rank), skinny_bytes(m, k, n, rank)
             tflops, gbs = flops / (ms * 1e-3) / 1e12, nbytes / (ms * 1e-3) / 1e9
             bound = "hbm" if flops / nbytes < BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma"
             frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tflops / BF16_PEAK_TFLOPS
-            results[f"{k}->{n} M{m}"] = {"ms": round(ms, 4), "TFLOP/s": round(tflops, 2), "GB/s": round(gbs, 1),
-                                         "bound": bound, "frac": round(frac, 4)}
-            log(f"  {k}->{n} M={m:6d}: {ms:8.3f} ms  {tflops:8.2f} TFLOP/s  {gbs:8.1f} GB/s  "
-                f"{bound} {100 * frac:.1f}%")
+            results[f"{k}->{n} M{m}"] = {"ms": round(ms, 4), "gpu_ms": round(gpu_ms, 4), "TFLOP/s": round(tflops, 2),
+                                         "GB/s": round(gbs, 1), "bound": bound, "frac": round(frac, 4)}
+            log(f"  {k}->{n} M={m:6d}: {ms:8.3f} ms (GPU {gpu_ms:.3f} ms)  {tflops:8.2f} TFLOP/s  "
+                f"{gbs:8.1f} GB/s  {bound} {100 * frac:.1f}%")
             del x, dy
         del module
         torch.cuda.empty_cache()

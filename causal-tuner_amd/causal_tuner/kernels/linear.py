@@ -509,7 +509,7 @@ class _LoRAGroup(torch.autograd.Function):
     def forward(ctx, x, dtype, tile, states, cosine, sine, head_dim, residual, *parameters):
         count = len(states)
         flat = x.reshape(-1, x.shape[-1]).to(dtype)
-        element = torch.empty((), dtype=dtype).element_size()
+        element = dtype.itemsize
         step, keep = _plan_rows(len(flat), tile, _KEEP_BUDGET.get(),
                                 group_row_bytes(parameters, count, element, head_dim))
         ctx.dtype, ctx.states, ctx.head_dim, ctx.step = dtype, states, head_dim, step
