@@ -172,6 +172,15 @@ def _mm_bf16(left, right, out, *, add=False):
     target.finish()
 
 
+def product(left, right, out):
+    """out = left right in the operands' dtype: ct_gemm for bf16 device operands (fp32
+    accumulation, one rounding), torch.mm otherwise (the reference's product)."""
+    if _device_bf16(left, right, out):
+        _mm_bf16(left, right, out)
+    else:
+        torch.mm(left, right, out=out)
+
+
 # ----------------------------------------------------------------------------- operators
 def cast_all(tensors, dtype, outputs=None):
     """[t.to(dtype) for t in tensors], with the fp32 device tensors that go to bf16 rounded

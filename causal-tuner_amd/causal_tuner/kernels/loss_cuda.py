@@ -14,6 +14,11 @@ over the supervised rows (`_SupervisedRows`), with one logits buffer for every t
 logits = x head^T (the BLAS library's GEMM through torch.mm), the fused CE over them, then
 d head += derivative^T x (`linear.accumulate`: fp32 output) and d hidden = derivative head
 for the tile's rows. Its backward only scales the cached gradients.
+
+d hidden reduces over the whole vocabulary into a [tile, d] output; for bf16 it runs
+ct_gemm, which splits that reduction across the GPU (fixed-order fp32 partials): 1.6-3.4x
+faster than hipBLASLt at 16-2048 rows of a 49152 x 2048 head on MI355X. The logits product
+has a short reduction and a wide output, where hipBLASLt is as fast, and stays on torch.mm.
 """
 
 import torch
@@ -102,7 +107,7 @@ class FusedProjectionLoss(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, hidden, head, targets, weights, tile, dtype, reuse, active):
-        from .linear import accumulate
+        from .linear import accumulate, product
         h = hidden.reshape(-1, hidden.shape[-1])
         rows = _SupervisedRows(active, h, targets.flatten(), weights.flatten(), tile)
         need_dh, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
@@ -141,14 +146,14 @@ class FusedProjectionLoss(torch.autograd.Function):
                 if dh is None:
                     continue
                 if in_place:
-                    torch.mm(logits, matrix, out=dh[where])
+                    product(logits, matrix, dh[where])
                     continue
-                product = staging[:size]
-                torch.mm(logits, matrix, out=product)
+                tile_dh = staging[:size]
+                product(logits, matrix, tile_dh)
                 if rows.interval:
-                    dh[where].copy_(product)
+                    dh[where].copy_(tile_dh)
                 else:
-                    dh.index_copy_(0, where, product.to(dh.dtype))
+                    dh.index_copy_(0, where, tile_dh.to(dh.dtype))
         if dh is not None:
             rows.clear_unsupervised(dh, holds_hidden=reuse)
         if reuse:

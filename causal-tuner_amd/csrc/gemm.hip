@@ -1086,19 +1086,26 @@ constexpr int kTileEdge[3] = {256, 128, 64};
 // rows on one ct_nf4_dequant pass into the workspace (the reference's materialize) plus
 // the dense GEMM is faster. Both give identical results.
 constexpr int64_t kMaterializeRows = CT_MATERIALIZE_ROWS;
-// Rows between the few-row kernels (m <= 64) and kMaterializeRows: the output alone
-// leaves most CUs idle, so the 256 x 256 fast runner splits the reduction and the fp32
-// partials are added in split order (with bias and beta) by reduce_splits. The split
-// count depends only on the shapes.
+// Reductions at least this long keep the split route from kMaterializeRows rows on.
+constexpr int64_t kLongReduction = 12288;
+// Rows between the few-row kernels (m <= 64) and kMaterializeRows, and more rows with a
+// reduction of at least kLongReduction: the output leaves the 256 x 256 grid short of one
+// round, so the fast runner splits the reduction and the fp32 partials are added in split
+// order (with bias and beta) by reduce_splits. Past kMaterializeRows the alternative is
+// the 128 x 128 or 64 x 64 grid over the whole reduction, which runs at half the rate or
+// less (measured on MI355X at 512-4096 rows and 12288-49152 reductions: 1.2-2.8x slower
+// than the split); shorter reductions there pay too much for the partials' traffic. The
+// split count depends only on the shapes.
 int mid_splits(int64_t m, int64_t n, int64_t ktot) {
-    if (m <= 64 || m >= kMaterializeRows || n <= 0) return 1;
+    if (m <= 64 || n <= 0) return 1;
+    const int64_t tiles = cdiv(m, 256) * cdiv(n, 256);
+    if (m >= kMaterializeRows && (ktot < kLongReduction || tiles >= 256)) return 1;
     // One round of the one-per-CU 256 x 256 workgroups: a partial second round would
     // take as long as the first.
-    const int64_t tiles = cdiv(m, 256) * cdiv(n, 256);
     int64_t s = 256 / tiles;
     const int64_t cap = cdiv(ktot, kBK) / 8;  // at least 8 k-tiles per split
     if (s > cap) s = cap;
-    if (s > 16) s = 16;
+    if (s > 32) s = 32;
     return (int)(s < 1 ? 1 : s);
 }
 
@@ -1221,8 +1228,8 @@ int64_t total_tiles(const GemmParams &p) {
 #define CT_LAYOUT(a0, b0, a1, b1) \
     (((a0) << 12) | ((b0) << 8) | ((a1) << 4) | (b1))
 
-// Split count of the mid-size route (65..511 rows: fp32 split partials of the 256 x 256
-// runner, then a reduction), or 1 when the problem does not take it.
+// Split count of the split route (fp32 split partials of the 256 x 256 runner, then a
+// reduction; the shapes mid_splits takes), or 1 when the problem does not take it.
 int mid_split_route(const Problem &pr) {
     const GemmParams &p = pr.p;
     if (pr.splits != 1 || pr.out != CT_BF16 || p.group_tiles != 0 || p.m <= 64) return 1;
@@ -1409,8 +1416,8 @@ hipError_t run_reduction(Problem pr, void *out, int64_t ldo, int add, void *ws, 
 int to_status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
 
 // Workspace a problem can use for split partials: few rows (the skinny kernels) or the
-// rows between them and kMaterializeRows (mid_splits). Only the shapes and source kinds
-// matter, so the operands need not exist yet.
+// split route (mid_splits). Only the shapes and source kinds matter, so the operands need
+// not exist yet.
 int64_t problem_workspace(int64_t m, int64_t n, const int64_t k[2], int nseg, const int src_b[2]) {
     if (m > 64) {
         const int s = mid_splits(m, n, k[0] + (nseg > 1 ? k[1] : 0));

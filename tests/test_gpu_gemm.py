@@ -138,3 +138,30 @@ def test_few_row_split_reduction_is_deterministic(m, n, k, trans_b):
     for c in (outs[0], outs[2]):
         worst, norm = _err(c, want)
         assert worst <= 8e-3 and norm <= 4e-3, (worst, norm)
+
+
+@pytest.mark.parametrize("m,n,k,trans_b", [(128, 2048, 49152, 0), (96, 1000, 13000, 1), (512, 2048, 16384, 1),
+                                           (1024, 2048, 12288, 0), (600, 1032, 20000, 0)])
+def test_long_reduction_split_is_deterministic(m, n, k, trans_b):
+    """An output short of one round of 256 x 256 tiles over a long reduction (the loss's
+    d hidden = derivative head, a 49152-long reduction into [tile, 2048]) takes the split
+    route, past 511 rows too: the workspace query asks for the partials, repeated calls
+    agree bit for bit, and the result matches a float64 product of the same bf16 operands
+    within bf16 rounding (also without a workspace, where the reduction is not split)."""
+    lib = _native.library()
+    a, abase, lda = _operand(m, k, False)
+    b, bbase, ldb = _operand(k, n, bool(trans_b))
+    need = lib.ct_gemm_workspace(m, n, k, 0, trans_b, _native.CT_BF16)
+    assert need >= 2 * m * n * 4
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    outs = []
+    for workspace, size in ((ws.data_ptr(), need), (ws.data_ptr(), need), (None, 0)):
+        c = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+        assert lib.ct_gemm(abase.data_ptr(), lda, 0, bbase.data_ptr(), ldb, trans_b, c.data_ptr(), n,
+                           _native.CT_BF16, None, 0, m, n, k, workspace, size, _native.stream_of(c)) == 0
+        outs.append(c)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    want = a.double() @ b.double()
+    for c in (outs[0], outs[2]):
+        worst, norm = _err(c, want)
+        assert worst <= 8e-3 and norm <= 4e-3, (worst, norm)
