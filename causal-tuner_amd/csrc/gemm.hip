@@ -1493,12 +1493,14 @@ extern "C" int ct_nf4_fused_supported(const ct_nf4_weight *w) { return nf4_fusab
 namespace ct {
 namespace {
 // Rank-r products (narrow outputs: r columns, or up to 1024 for a group's stacked factors;
-// many rows; a long reduction): when 128 x 128 tiles give less than one workgroup per CU,
-// the reduction is split 2 to 4 ways (about 512 workgroups, two per CU). Measured on
-// MI355X: at 8192 rows and 256 columns 20-25% faster than 64-wide tiles for reductions of
-// 11008; at 4096 rows the stacked q/k/v and gate/up products likewise.
+// many rows; a reduction of at least 4096): when 128 x 128 tiles give less than one
+// workgroup per CU, the reduction is split 2 to 4 ways (about 512 workgroups, two per CU).
+// Measured on MI355X: at 8192 rows and 256 columns 20-25% faster than 64-wide tiles for
+// reductions of 11008, at 4096 rows 27-40% faster for 8192. Over 2048 the unsplit 64 x 64
+// grid is faster (4096 rows: 12.5 against 20.3 us at 256 columns, 24.9 against 30.7 at
+// 768, 18.7 against 25.4 at 512).
 bool lowrank_split(int64_t m, int64_t n, int64_t k, int *tile, int *splits) {
-    if (n > 1024 || m < 4096 || k < 2048) return false;
+    if (n > 1024 || m < 4096 || k < 4096) return false;
     const int64_t tiles = cdiv(m, 128) * cdiv(n, 128);
     if (tiles >= 256) return false;
     int64_t s = 512 / tiles;
@@ -1875,13 +1877,20 @@ ParamPlan param_plan(int64_t m, int64_t n, int64_t k, int64_t r) {
         pl.splits = 1;
         return pl;
     }
+    // Outputs that give the 256 x 256 grid fewer than 32 tiles would need more than 8
+    // splits to fill the GPU: 128 x 128 tiles fill it with fewer, shorter partials
+    // (measured on MI355X: 2048 x 2048 at 4096 tokens 41.5 -> 30.9 us, the k/v projections'
+    // 2048 x 128 at 4096 tokens 35.2 -> 23.3 us, 4096 x 128 at 8192 53.5 -> 47.6 us).
+    if (pl.tile == TILE_256 && cdiv(r, 256) * (cdiv(k, 256) + cdiv(n, 256)) < 32) pl.tile = TILE_128;
     const int64_t e = kTileEdge[pl.tile];
     pl.gt = (int)cdiv(k, e);
     pl.width = pl.gt * e + n;
     const int64_t tiles = cdiv(r, e) * (pl.gt + cdiv(n, e));
     const int64_t ktiles = cdiv(m, kBK);
     // At most 8 splits: beyond that the partial sums' traffic costs more than the extra
-    // workgroups gain (measured on MI355X at 8192 tokens).
+    // workgroups gain (measured on MI355X at 8192 tokens). At most one workgroup per CU:
+    // 128 x 128 tiles run two per CU, and a count just past 256 leaves some CUs with two
+    // and the rest with one.
     int64_t s = 256 / (tiles > 0 ? tiles : 1);
     const int64_t cap = ktiles / 8 > 1 ? ktiles / 8 : 1;
     if (s > cap) s = cap;

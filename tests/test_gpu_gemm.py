@@ -115,7 +115,7 @@ def test_gemm_runs_on_the_callers_stream():
 
 @pytest.mark.parametrize("m,n,k,trans_b", [(16, 256, 6144, 1), (7, 256, 24576, 0), (64, 128, 4096, 1),
                                            (33, 512, 2048, 0), (8192, 256, 4096, 1), (8192, 256, 11008, 0),
-                                           (4100, 200, 2056, 1)])
+                                           (4100, 200, 4104, 1)])
 def test_few_row_split_reduction_is_deterministic(m, n, k, trans_b):
     """m <= 64, or a rank-r product (n <= 256) over many rows, with a workspace splits the
     reduction across workgroups; the fp32 partials add in split order, so repeated calls
