@@ -1087,14 +1087,15 @@ constexpr int kTileEdge[3] = {256, 128, 64};
 // the dense GEMM is faster. Both give identical results.
 constexpr int64_t kMaterializeRows = CT_MATERIALIZE_ROWS;
 // Reductions at least this long keep the split route from kMaterializeRows rows on.
-constexpr int64_t kLongReduction = 12288;
+constexpr int64_t kLongReduction = 8192;
 // Rows between the few-row kernels (m <= 64) and kMaterializeRows, and more rows with a
 // reduction of at least kLongReduction: the output leaves the 256 x 256 grid short of one
 // round, so the fast runner splits the reduction and the fp32 partials are added in split
 // order (with bias and beta) by reduce_splits. Past kMaterializeRows the alternative is
 // the 128 x 128 or 64 x 64 grid over the whole reduction, which runs at half the rate or
 // less (measured on MI355X at 512-4096 rows and 12288-49152 reductions: 1.2-2.8x slower
-// than the split); shorter reductions there pay too much for the partials' traffic. The
+// than the split; 6-9% slower at 2048-4096 rows, 2048 columns and 8448); shorter
+// reductions there pay too much for the partials' traffic (2048: 25% slower split). The
 // split count depends only on the shapes.
 int mid_splits(int64_t m, int64_t n, int64_t ktot) {
     if (m <= 64 || n <= 0) return 1;
