@@ -1022,6 +1022,64 @@ __global__ __launch_bounds__(256) void reduce_splits(const float *__restrict__ w
     }
 }
 
+// reduce_splits with 16-byte accesses, eight columns per thread, the same sums in the same
+// order (identical results). Needs cols % 8 == 0, 16-byte aligned partials, output and
+// bias, and ldo % 8 == 0. Grid: (column blocks of 2048, rows).
+template <int OUT>
+__global__ __launch_bounds__(256) void reduce_splits_vec(const float *__restrict__ ws, int splits, int64_t stride,
+                                                         int64_t rows, int64_t cols, void *out, int64_t ldo, int add,
+                                                         const uint16_t *__restrict__ bias) {
+    const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8, r = blockIdx.y;
+    if (c >= cols) return;
+    const float *src = ws + r * cols + c;
+    float s[8];
+    for (int z0 = 0; z0 < splits; z0 += 4) {
+        float4 v[4][2];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (z0 + j < splits) {
+                const float4 *q = reinterpret_cast<const float4 *>(src + (z0 + j) * stride);
+                v[j][0] = q[0];
+                v[j][1] = q[1];
+            }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (z0 + j < splits) {
+                const float x[8] = {v[j][0].x, v[j][0].y, v[j][0].z, v[j][0].w,
+                                    v[j][1].x, v[j][1].y, v[j][1].z, v[j][1].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s[e] = (z0 + j == 0) ? x[e] : s[e] + x[e];
+            }
+    }
+    if (bias) {
+        const uint4 b = *reinterpret_cast<const uint4 *>(bias + c);
+        const uint32_t w[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[e] += bf16_to_f32((uint16_t)(w[e / 2] >> (16 * (e & 1))));
+    }
+    if constexpr (OUT == CT_F32) {
+        float4 *o = reinterpret_cast<float4 *>(static_cast<float *>(out) + r * ldo + c);
+        float4 lo = make_float4(s[0], s[1], s[2], s[3]), hi = make_float4(s[4], s[5], s[6], s[7]);
+        if (add) {
+            const float4 a0 = o[0], a1 = o[1];
+            lo = make_float4(s[0] + a0.x, s[1] + a0.y, s[2] + a0.z, s[3] + a0.w);
+            hi = make_float4(s[4] + a1.x, s[5] + a1.y, s[6] + a1.z, s[7] + a1.w);
+        }
+        o[0] = lo;
+        o[1] = hi;
+    } else {
+        uint4 *o = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + r * ldo + c);
+        if (add) {
+            const uint4 q = *o;
+            const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[e] = s[e] + bf16_to_f32((uint16_t)(w[e / 2] >> (16 * (e & 1))));
+        }
+        *o = make_uint4(pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3]), pack_bf16x2(s[4], s[5]),
+                        pack_bf16x2(s[6], s[7]));
+    }
+}
+
 // dst[c][r] = src[r][c] for a bf16 [rows, cols] matrix (the rank-r factor a of the dx
 // GEMM, so that it enters as a reduction-contiguous operand); 32 x 32 tiles through LDS.
 __global__ __launch_bounds__(256) void transpose_bf16(const uint16_t *__restrict__ src, int64_t rows, int64_t cols,
@@ -1072,6 +1130,74 @@ __global__ __launch_bounds__(256) void reduce_param(const float *__restrict__ ws
             if (z0 + j < splits) s = (z0 + j == 0) ? v[j] : s + v[j];
     }
     *o = add ? s + *o : s;
+}
+
+// reduce_param over 32 x 64 tiles (rows i, columns c) with 16-byte accesses and the same
+// sums in the same order (identical results): a dA tile is written row by row; a dB^T tile
+// goes through LDS so that dB [n, r] is written along r, 32 contiguous floats per column
+// (the per-element kernel writes it with a stride of r floats). Needs width, k and r
+// multiples of 8, gcols a multiple of 64, and 16-byte aligned partials, da and db.
+// Grid: (cdiv(width, 64), cdiv(r, 32)).
+__global__ __launch_bounds__(256) void reduce_param_tiled(const float *__restrict__ ws, int splits, int64_t stride,
+                                                          int64_t r, int64_t width, int64_t gcols, int64_t k,
+                                                          int64_t n, float *da, float *db, int add) {
+    __shared__ float tile[64][33];
+    const int t = threadIdx.x, li = t >> 3, lc = (t & 7) * 8;
+    const int64_t i0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 64;
+    const int64_t i = i0 + li, c = c0 + lc;
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (i < r && c < width) {
+        const float *src = ws + i * width + c;
+        for (int z0 = 0; z0 < splits; z0 += 4) {
+            float4 v[4][2];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (z0 + j < splits) {
+                    const float4 *q = reinterpret_cast<const float4 *>(src + (z0 + j) * stride);
+                    v[j][0] = q[0];
+                    v[j][1] = q[1];
+                }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (z0 + j < splits) {
+                    const float x[8] = {v[j][0].x, v[j][0].y, v[j][0].z, v[j][0].w,
+                                        v[j][1].x, v[j][1].y, v[j][1].z, v[j][1].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) s[e] = (z0 + j == 0) ? x[e] : s[e] + x[e];
+                }
+        }
+    }
+    if (c0 < gcols) {  // the whole tile is dA (gcols is a multiple of 64)
+        if (i >= r || c >= k) return;
+        float4 *o = reinterpret_cast<float4 *>(da + i * k + c);
+        float4 lo = make_float4(s[0], s[1], s[2], s[3]), hi = make_float4(s[4], s[5], s[6], s[7]);
+        if (add) {
+            const float4 a0 = o[0], a1 = o[1];
+            lo = make_float4(s[0] + a0.x, s[1] + a0.y, s[2] + a0.z, s[3] + a0.w);
+            hi = make_float4(s[4] + a1.x, s[5] + a1.y, s[6] + a1.z, s[7] + a1.w);
+        }
+        o[0] = lo;
+        o[1] = hi;
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[lc + e][li] = s[e];
+    __syncthreads();
+    const int cc = t >> 2, ig = (t & 3) * 8;
+    const int64_t col = c0 - gcols + cc, row = i0 + ig;
+    if (col >= n || row >= r) return;
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = tile[cc][ig + e];
+    float4 *o = reinterpret_cast<float4 *>(db + col * r + row);
+    float4 lo = make_float4(y[0], y[1], y[2], y[3]), hi = make_float4(y[4], y[5], y[6], y[7]);
+    if (add) {
+        const float4 a0 = o[0], a1 = o[1];
+        lo = make_float4(y[0] + a0.x, y[1] + a0.y, y[2] + a0.z, y[3] + a0.w);
+        hi = make_float4(y[4] + a1.x, y[5] + a1.y, y[6] + a1.z, y[7] + a1.w);
+    }
+    o[0] = lo;
+    o[1] = hi;
 }
 
 // ------------------------------------------------------------------------ host side
@@ -1229,6 +1355,20 @@ int64_t total_tiles(const GemmParams &p) {
 #define CT_LAYOUT(a0, b0, a1, b1) \
     (((a0) << 12) | ((b0) << 8) | ((a1) << 4) | (b1))
 
+// out (+)= sum of the fp32 split partials in ws (+ bias), in split order: 16-byte accesses
+// where the layout allows them (the same sums either way).
+template <int OUT>
+hipError_t launch_reduce(const float *ws, int splits, int64_t stride, int64_t rows, int64_t cols, void *out,
+                         int64_t ldo, int add, const uint16_t *bias, hipStream_t s) {
+    if (cols % 8 == 0 && ldo % 8 == 0 && aligned16(ws) && aligned16(out) && (!bias || aligned16(bias)))
+        reduce_splits_vec<OUT><<<dim3((unsigned)cdiv(cols, 2048), (unsigned)rows), 256, 0, s>>>(
+            ws, splits, stride, rows, cols, out, ldo, add, bias);
+    else
+        reduce_splits<OUT><<<dim3((unsigned)cdiv(cols, 256), (unsigned)rows), 256, 0, s>>>(ws, splits, stride, rows,
+                                                                                          cols, out, ldo, add, bias);
+    return hipGetLastError();
+}
+
 // Split count of the split route (fp32 split partials of the 256 x 256 runner, then a
 // reduction; the shapes mid_splits takes), or 1 when the problem does not take it.
 int mid_split_route(const Problem &pr) {
@@ -1301,9 +1441,8 @@ hipError_t run(Problem &pr, hipStream_t s) {
         q.p.bias = nullptr;
         const hipError_t e = run(q, s);
         if (e != hipSuccess) return e;
-        reduce_splits<CT_BF16><<<dim3((unsigned)cdiv(p.n, 256), (unsigned)p.m), 256, 0, s>>>(
-            static_cast<const float *>(pr.ws), splits, p.m * p.n, p.m, p.n, p.c, p.ldc, p.beta, p.bias);
-        return hipGetLastError();
+        return launch_reduce<CT_BF16>(static_cast<const float *>(pr.ws), splits, p.m * p.n, p.m, p.n, p.c, p.ldc,
+                                      p.beta, p.bias, s);
     }
     if (pr.splits == 1 && pr.out == CT_BF16 && p.m <= 64) {
         // Few rows: the workgroup streams the weight with its 8 waves splitting the reduction.
@@ -1404,14 +1543,11 @@ hipError_t run_reduction(Problem pr, void *out, int64_t ldo, int add, void *ws, 
     pr.vec = pr.vec && aligned16(ws) && p.n % 8 == 0;
     hipError_t e = run(pr, s);
     if (e != hipSuccess) return e;
-    const dim3 grid((unsigned)cdiv(p.n, 256), (unsigned)p.m);
     if (final_out == CT_F32)
-        reduce_splits<CT_F32><<<grid, 256, 0, s>>>(static_cast<float *>(ws), splits, p.split_stride, p.m, p.n,
-                                                   out, ldo, add, nullptr);
-    else
-        reduce_splits<CT_BF16><<<grid, 256, 0, s>>>(static_cast<float *>(ws), splits, p.split_stride, p.m,
-                                                    p.n, out, ldo, add, nullptr);
-    return hipGetLastError();
+        return launch_reduce<CT_F32>(static_cast<float *>(ws), splits, p.split_stride, p.m, p.n, out, ldo, add,
+                                     nullptr, s);
+    return launch_reduce<CT_BF16>(static_cast<float *>(ws), splits, p.split_stride, p.m, p.n, out, ldo, add, nullptr,
+                                  s);
 }
 
 int to_status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
@@ -1970,9 +2106,13 @@ extern "C" int ct_parameter_gradients(const void *x, int64_t ldx, const void *dy
     hipError_t e = run(pr, stream);
     if (e == hipSuccess) {
         const int64_t gcols = k > 0 ? (int64_t)pl.gt * kTileEdge[pl.tile] : 0;
-        const dim3 grid((unsigned)cdiv(pl.width, 256), (unsigned)r);
-        reduce_param<<<grid, 256, 0, stream>>>(static_cast<const float *>(workspace), pl.splits, r * pl.width, r,
-                                               pl.width, gcols, k, n, da, db, add);
+        if (pl.width % 8 == 0 && k % 8 == 0 && r % 8 == 0 && gcols % 64 == 0 && aligned16(workspace) &&
+            (k == 0 || aligned16(da)) && (n == 0 || aligned16(db)))
+            reduce_param_tiled<<<dim3((unsigned)cdiv(pl.width, 64), (unsigned)cdiv(r, 32)), 256, 0, stream>>>(
+                static_cast<const float *>(workspace), pl.splits, r * pl.width, r, pl.width, gcols, k, n, da, db, add);
+        else
+            reduce_param<<<dim3((unsigned)cdiv(pl.width, 256), (unsigned)r), 256, 0, stream>>>(
+                static_cast<const float *>(workspace), pl.splits, r * pl.width, r, pl.width, gcols, k, n, da, db, add);
         e = hipGetLastError();
     }
     profile_close(slot, stream, 2.0 * m * r * (double)(k + n));

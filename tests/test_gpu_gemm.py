@@ -165,3 +165,28 @@ def test_long_reduction_split_is_deterministic(m, n, k, trans_b):
     for c in (outs[0], outs[2]):
         worst, norm = _err(c, want)
         assert worst <= 8e-3 and norm <= 4e-3, (worst, norm)
+
+
+@pytest.mark.parametrize("m,n,k", [(200, 512, 4096), (96, 2048, 49152), (600, 1032, 20000)])
+def test_split_route_with_bias_and_accumulation(m, n, k):
+    """The split route's reduction adds the bias and, with beta, the previous output (bf16)
+    after the partials, in split order: against float64 products of the same operands."""
+    lib = _native.library()
+    a, abase, lda = _operand(m, k, False)
+    b, bbase, ldb = _operand(k, n, True)
+    bias = (torch.randn(n, device="cuda") * 0.5).to(torch.bfloat16)
+    need = lib.ct_gemm_workspace(m, n, k, 0, 1, _native.CT_BF16)
+    assert need >= 2 * m * n * 4
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    c = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+    assert lib.ct_gemm(abase.data_ptr(), lda, 0, bbase.data_ptr(), ldb, 1, c.data_ptr(), n, _native.CT_BF16,
+                       bias.data_ptr(), 0, m, n, k, ws.data_ptr(), need, _native.stream_of(c)) == 0
+    product = a.double() @ b.double()
+    want = product + bias.double()
+    worst, norm = _err(c, want)
+    assert worst <= 8e-3 and norm <= 4e-3, (worst, norm)
+    first = c.clone()
+    assert lib.ct_gemm(abase.data_ptr(), lda, 0, bbase.data_ptr(), ldb, 1, c.data_ptr(), n, _native.CT_BF16,
+                       None, 1, m, n, k, ws.data_ptr(), need, _native.stream_of(c)) == 0
+    worst, norm = _err(c, first.double() + product)
+    assert worst <= 8e-3 and norm <= 4e-3, (worst, norm)
