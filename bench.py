@@ -339,10 +339,10 @@ FAMILIES = {
     "lowrank": ("CT_PROF_LOWRANK", "rank-r products inside the entry points (xa = x a^T, low = dy b)"),
     "dequant": ("CT_PROF_DEQUANT", "in-step NF4 decode of the base weights (ct_nf4_dequant, bytes not flops)"),
 }
-# The dx family is one kernel instantiation for every C3 projection (all reach 256x256 tiles).
-# At 8192 rows the dx GEMM runs on the transposed decoded weight, so both big GEMM families
-# share one kernel instantiation.
-KERNEL_NAMES = {"dx_gemm": "gemm_big8<KC, KC, KC, KC> (dx on w^T and a^T)",
+# The dx family is one kernel instantiation for every C3 projection (all reach 256x256 tiles):
+# at 8192 rows the dx GEMM runs on the transposed decoded weight, reduction-contiguous, and
+# reads a [r, k] of its second segment through the transposing loader.
+KERNEL_NAMES = {"dx_gemm": "gemm_big8<KC, KC, KC, KS> (dx on w^T and a)",
                 "fwd_gemm": "gemm_big8<KC, KC, KC, KC> (q,o,gate,up,down) + gemm_small<64,64,...> (k, v)"}
 
 
@@ -370,9 +370,8 @@ def pmc_summary(fetch_csv, write_csv, family, mib):
     """Per-launch HBM traffic of a kernel family from two rocprofv3 --pmc runs (FETCH_SIZE,
     WRITE_SIZE, KiB per dispatch), each scaled by the same counter's reading for the copy
     probe of `mib` MiB; written to profiles/<family>_traffic.json."""
-    # Forward and dx share the instantiation: the figure averages both families' launches.
     # The few-row kernels (bench.py --skinny-only): both C5 shapes move the same weight bytes.
-    patterns = {"dx_gemm": "gemm_big8<0, 0, 0, 0, 2>", "fwd_gemm": "gemm_big8<0, 0, 0, 0, 2>",
+    patterns = {"dx_gemm": "gemm_big8<0, 0, 0, 1, 2>", "fwd_gemm": "gemm_big8<0, 0, 0, 0, 2>",
                 "skinny_fwd": "rows_kernel<2, 0,", "skinny_dx": "cols_kernel<3, 1,"}
     copy_bytes = mib << 20
 

@@ -1080,22 +1080,6 @@ __global__ __launch_bounds__(256) void reduce_splits_vec(const float *__restrict
     }
 }
 
-// dst[c][r] = src[r][c] for a bf16 [rows, cols] matrix (the rank-r factor a of the dx
-// GEMM, so that it enters as a reduction-contiguous operand); 32 x 32 tiles through LDS.
-__global__ __launch_bounds__(256) void transpose_bf16(const uint16_t *__restrict__ src, int64_t rows, int64_t cols,
-                                                      uint16_t *__restrict__ dst) {
-    __shared__ uint16_t t[32][33];
-    const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
-    const int x = threadIdx.x & 31, y = threadIdx.x >> 5;  // 8 rows per pass
-#pragma unroll
-    for (int i = 0; i < 32; i += 8)
-        if (r0 + y + i < rows && c0 + x < cols) t[y + i][x] = src[(r0 + y + i) * cols + c0 + x];
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 32; i += 8)
-        if (c0 + y + i < cols && r0 + x < rows) dst[(c0 + y + i) * rows + r0 + x] = t[x][y + i];
-}
-
 // A fill kernel rather than hipMemsetAsync, so the call stays safe inside graph capture.
 __global__ __launch_bounds__(256) void fill_zero(float *p, int64_t count) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -1464,6 +1448,8 @@ hipError_t run(Problem &pr, hipStream_t s) {
             return launch_vec_out<SRC_KC, SRC_KC, SRC_KC, SRC_KC>(pr, tile, s);
         case CT_LAYOUT(SRC_KC, SRC_KS, SRC_KC, SRC_KS):
             return launch_vec_out<SRC_KC, SRC_KS, SRC_KC, SRC_KS>(pr, tile, s);
+        case CT_LAYOUT(SRC_KC, SRC_KC, SRC_KC, SRC_KS):  // dx on the transposed decode
+            return launch_vec_out<SRC_KC, SRC_KC, SRC_KC, SRC_KS>(pr, tile, s);
         case CT_LAYOUT(SRC_KS, SRC_KS, SRC_KS, SRC_KS):
             return launch_vec_out<SRC_KS, SRC_KS, SRC_KS, SRC_KS>(pr, tile, s);
         case CT_LAYOUT(SRC_KS, SRC_KC, SRC_KS, SRC_KC):
@@ -1867,8 +1853,8 @@ extern "C" int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, 
     const int sb[2] = {SRC_NF4T, SRC_KS};
     const int64_t main = problem_workspace(m, k, ks, r > 0 ? 2 : 1, sb);
     const int64_t rest = inner > main ? inner : main;
-    // Many rows: the decoded weight (transposed) and the transposed factor a come first.
-    return materialize_kind(nf4, m, k, n + r) ? weight_bytes(n, k) + weight_bytes(r, k) + rest : rest;
+    // Many rows: the decoded weight (transposed) comes first.
+    return materialize_kind(nf4, m, k, n + r) ? weight_bytes(n, k) + rest : rest;
 }
 
 extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_dense, const ct_nf4_weight *w_nf4,
@@ -1882,7 +1868,7 @@ extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_den
     if (epi.kind != CT_EPI_NONE && add) return -CT_EINVAL_LAYOUT;
     if (!dy || !dx || (!w_dense == !w_nf4) || (r > 0 && (!a || !b || !low))) return -CT_EINVAL_POINTER;
     if (lddy < n || lddx < k) return -CT_EINVAL_SHAPE;
-    const void *w_trans = nullptr, *a_trans = nullptr;  // w^T [k, n] and a^T [k, r] in the workspace
+    const void *w_trans = nullptr;  // w^T [k, n] in the workspace
     if (w_nf4) {
         const int st = validate_nf4(w_nf4);
         if (st) return st;
@@ -1891,22 +1877,13 @@ extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_den
             void *wbuf = nullptr;
             const int ws = take_weight(workspace, workspace_bytes, n, k, wbuf);
             if (ws) return ws;
-            if (nf4_transposable(w_nf4) && (r == 0 || (aligned16(a) && r % 8 == 0))) {
-                // Decode w^T [k, n] and transpose a to [k, r]: both operands of dx then run
-                // reduction-contiguous, on the forward GEMM's kernel.
-                void *abuf = nullptr;
-                const int wa = take_weight(workspace, workspace_bytes, r, k, abuf);
-                if (wa) return wa;
+            if (nf4_transposable(w_nf4)) {
+                // Decode w^T [k, n]: the main segment then runs reduction-contiguous on both
+                // operands, on the forward GEMM's kernel; a [r, k] enters the short second
+                // segment through the transposing loader.
                 const hipError_t dq = nf4_dequant_transposed(w_nf4, wbuf, stream);
                 if (dq != hipSuccess) return to_status(dq);
-                if (r > 0) {
-                    transpose_bf16<<<dim3((unsigned)cdiv(k, 32), (unsigned)cdiv(r, 32)), 256, 0, stream>>>(
-                        static_cast<const uint16_t *>(a), r, k, static_cast<uint16_t *>(abuf));
-                    const hipError_t te = hipGetLastError();
-                    if (te != hipSuccess) return to_status(te);
-                }
                 w_trans = wbuf;
-                a_trans = abuf;
             } else {
                 const int dq = ct_nf4_dequant(w_nf4, wbuf, CT_BF16, stream);
                 if (dq) return dq;
@@ -1930,7 +1907,7 @@ extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_den
     pr.p.seg[0].b = w_nf4 ? nf4_operand(w_nf4) : (w_trans ? dense(w_trans, n) : dense(w_dense, k));
     pr.p.seg[0].k = n;
     pr.p.seg[1].a = dense(low, r);
-    pr.p.seg[1].b = a_trans ? dense(a_trans, r) : dense(a, k);
+    pr.p.seg[1].b = dense(a, k);
     pr.p.seg[1].k = r;
     pr.p.nseg = r > 0 ? 2 : 1;
     pr.p.m = m;
@@ -1944,7 +1921,7 @@ extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_den
     pr.src[0] = SRC_KC;
     pr.src[1] = w_nf4 ? SRC_NF4T : (w_trans ? SRC_KC : SRC_KS);
     pr.src[2] = SRC_KC;
-    pr.src[3] = a_trans ? SRC_KC : SRC_KS;
+    pr.src[3] = SRC_KS;
     pr.out = CT_BF16;
     pr.splits = 1;
     pr.tile = -1;
