@@ -632,13 +632,24 @@ SkShape sk_shape(const GemmParams &p, bool columns, int64_t ws_floats) {
         groups = cdiv(p.n, 64 * sh.nb);
         min_steps = 4;
     }
-    // Whole rounds of resident workgroups: splits * groups a multiple of the target when
-    // the columns alone do not fill the GPU.
-    int64_t splits = groups >= target ? 1 : cdiv(target, groups);
+    // At most enough splits to fill the resident slots once when the columns alone do not
+    // fill the GPU; below that, the count that spreads the work most evenly over the CUs:
+    // the busiest CU holds ceil(s * groups / CUs) workgroups of 1/s of the reduction each,
+    // so a count just past a whole round costs a second round (measured on MI355X at 64
+    // rows: the 6144-wide dx 102.7 -> 65.5 us with 5 splits instead of 6, the 24576-long
+    // forward 83.2 -> 67.3 us with 5 instead of 6; at 16 rows the counts are unchanged).
+    int64_t limit = groups >= target ? 1 : cdiv(target, groups);
     const int64_t cap = steps / min_steps > 1 ? steps / min_steps : 1;
-    if (splits > cap) splits = cap;
-    if (splits > 64) splits = 64;
-    if (splits < 1) splits = 1;
+    if (limit > cap) limit = cap;
+    if (limit > 64) limit = 64;
+    int64_t splits = 1, busiest = cdiv(groups, kCUs);  // busiest CU's load x splits
+    for (int64_t s = 2; s <= limit; ++s) {
+        const int64_t load = cdiv(s * groups, kCUs);
+        if (load * splits < busiest * s) {  // load / s < busiest / splits
+            splits = s;
+            busiest = load;
+        }
+    }
     if (splits > 1 && ws_floats >= 0 && splits * p.m * p.n > ws_floats) splits = 1;
     sh.splits = (int)splits;
     return sh;
