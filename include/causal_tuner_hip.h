@@ -175,8 +175,10 @@ int ct_nf4_quantize(const void *w, int32_t w_dtype, int64_t n, int32_t blocksize
  *   B(k,n) = b[n*ldb + k]  (trans_b = 1)  or  b[k*ldb + n]  (trans_b = 0)
  * c_dtype is CT_BF16 (rounded once, RTNE) or CT_F32. bias may be null (bf16 [n]).
  *
- * Workspace (here and in ct_forward_linear / ct_input_gradient): with m <= 64 rows the
- * reduction may be split across workgroups, the fp32 partials going to the caller's
+ * Workspace (here and in ct_forward_linear / ct_input_gradient): with m <= 64 rows, with
+ * 65-511 rows, with a rank-r output (n <= 1024) over many rows and a reduction of at least
+ * 4096, and with a reduction of at least 8192 into an output short of one round of
+ * 256 x 256 tiles, the reduction may be split across workgroups, the fp32 partials going to the caller's
  * workspace and summed in a fixed order (results do not depend on timing). The *_workspace
  * query gives the size that allows the preferred split; a null or smaller workspace is
  * valid and only splits less (no split at all without one). The partials are written with
@@ -294,8 +296,10 @@ int ct_adamw_step(const ct_adamw_tensor *tensors, int64_t count, const int64_t *
  * weight is decoded tile by tile into LDS inside the GEMM (materialize fused away, which
  * needs ct_nf4_fused_supported(w_nf4), else -CT_EINVAL_LAYOUT). Both paths give results
  * bit-identical to ct_nf4_dequant's bf16 weight in the dense GEMM. Between 65 and 511
- * rows the reduction may be split across workgroups (fp32 partials in the workspace,
- * added in a fixed order); a weight without double quantization is then decoded first.
+ * rows, and past them when a reduction of at least 8192 leaves the output short of one
+ * round of 256 x 256 tiles, the reduction may be split across workgroups (fp32 partials
+ * in the workspace, added in a fixed order); a weight without double quantization is
+ * then decoded first.
  * x [m, k] (ldx), a bf16 [r, k], b bf16 [n, r], bias bf16 [n] or null, out [m, n] (ldo),
  * xa bf16 [m, r] (row pitch ldxa >= r). `epilogue` (may be null) is an elementwise step on
  * out (ct_epilogue). With xa_given != 0, xa already holds x a^T (a may
