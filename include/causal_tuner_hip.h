@@ -326,8 +326,9 @@ int ct_forward_linear(const void *x, int64_t ldx,
  * CT_STATIC_SCRATCH_BYTES per GPU (held from the library's load on that GPU until the process
  * ends) in place of the workspace. A problem whose ct_forward_linear_workspace exceeds
  * CT_STATIC_SCRATCH_BYTES returns -CT_EINVAL_WORKSPACE before anything is enqueued: 64 MiB
- * covers every few-row problem and the many-row ones whose decoded weight fits (up to
- * about 32 M weight elements). It calls no allocator. Every call on one GPU uses that GPU's
+ * covers every few-row problem and the many-row ones whose decoded weight, plus the
+ * split partials where the reduction is split, fits (up to about 32 M weight elements
+ * without a split). It calls no allocator. Every call on one GPU uses that GPU's
  * one array: calls that overlap on a GPU (two streams or threads) race and must be ordered
  * by the caller.
  */
