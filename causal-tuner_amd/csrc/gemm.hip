@@ -1685,15 +1685,23 @@ extern "C" int ct_gemm(const void *a, int64_t lda, int32_t trans_a, const void *
 
 namespace ct {
 namespace {
+// dx decodes its weight first from fewer rows than the forward: its loader, which decodes
+// the packed weight into the transposed layout, is the slower of the two fused loaders,
+// and from 384 rows the transposed decode plus the dense kernel is faster (measured on
+// MI355X at C5's shapes: 384 rows 318 -> 284 and 454 -> 305 us, 511 rows 330 -> 298 and
+// 466 -> 313 us; at 256 rows the fused loader stays faster, 198 against 233 us). The
+// forward's fused loader keeps up to kMaterializeRows (at 384-511 rows the two orders
+// are within 7% either way). Both orders give the same results.
+constexpr int64_t kMaterializeRowsDx = 384;
 // Also decoded first: a weight without double quantization (the fast runner's NF4 loader
 // needs the nested state) in a problem that splits its reduction, so that it takes the
 // same kernel and summation order as the bf16 weight it decodes to.
-bool materialize_nf4(const ct_nf4_weight *w, int64_t m, int64_t n_out, int64_t ktot) {
-    return w && (m >= kMaterializeRows || (!w->nested && mid_splits(m, n_out, ktot) > 1));
+bool materialize_nf4(const ct_nf4_weight *w, int64_t m, int64_t n_out, int64_t ktot, int64_t from) {
+    return w && (m >= from || (!w->nested && mid_splits(m, n_out, ktot) > 1));
 }
 // Workspace queries: nf4 is 0 (bf16 weight), 1 (NF4, double-quantized) or 2 (NF4, plain).
-bool materialize_kind(int32_t nf4, int64_t m, int64_t n_out, int64_t ktot) {
-    return nf4 && (m >= kMaterializeRows || (nf4 == 2 && mid_splits(m, n_out, ktot) > 1));
+bool materialize_kind(int32_t nf4, int64_t m, int64_t n_out, int64_t ktot, int64_t from) {
+    return nf4 && (m >= from || (nf4 == 2 && mid_splits(m, n_out, ktot) > 1));
 }
 int64_t weight_bytes(int64_t n, int64_t k) { return (n * k * 2 + 255) & ~int64_t{255}; }
 
@@ -1776,7 +1784,7 @@ extern "C" int64_t ct_forward_linear_workspace(int64_t m, int64_t n, int64_t k, 
     const int sb[2] = {SRC_NF4, SRC_KC};  // the dense weight (KC) has the same split shape
     const int64_t main = problem_workspace(m, n, ks, r > 0 ? 2 : 1, sb);
     const int64_t rest = inner > main ? inner : main;  // the two launches run in order on one stream
-    return materialize_kind(nf4, m, n, k + r) ? weight_bytes(n, k) + rest : rest;
+    return materialize_kind(nf4, m, n, k + r, kMaterializeRows) ? weight_bytes(n, k) + rest : rest;
 }
 
 extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense, const ct_nf4_weight *w_nf4,
@@ -1794,7 +1802,7 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
         const int st = validate_nf4(w_nf4);
         if (st) return st;
         if (w_nf4->rows != n || w_nf4->cols != k) return -CT_EINVAL_SHAPE;
-        if (materialize_nf4(w_nf4, m, n, k + r)) {
+        if (materialize_nf4(w_nf4, m, n, k + r, kMaterializeRows)) {
             void *wbuf = nullptr;
             const int ws = take_weight(workspace, workspace_bytes, n, k, wbuf);
             if (ws) return ws;
@@ -1854,7 +1862,7 @@ extern "C" int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, 
     const int64_t main = problem_workspace(m, k, ks, r > 0 ? 2 : 1, sb);
     const int64_t rest = inner > main ? inner : main;
     // Many rows: the decoded weight (transposed) comes first.
-    return materialize_kind(nf4, m, k, n + r) ? weight_bytes(n, k) + rest : rest;
+    return materialize_kind(nf4, m, k, n + r, kMaterializeRowsDx) ? weight_bytes(n, k) + rest : rest;
 }
 
 extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_dense, const ct_nf4_weight *w_nf4,
@@ -1873,7 +1881,7 @@ extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_den
         const int st = validate_nf4(w_nf4);
         if (st) return st;
         if (w_nf4->rows != n || w_nf4->cols != k) return -CT_EINVAL_SHAPE;
-        if (materialize_nf4(w_nf4, m, k, n + r)) {
+        if (materialize_nf4(w_nf4, m, k, n + r, kMaterializeRowsDx)) {
             void *wbuf = nullptr;
             const int ws = take_weight(workspace, workspace_bytes, n, k, wbuf);
             if (ws) return ws;

@@ -91,3 +91,18 @@ def test_parameter_gradients_unsplit(m, n, k, r, tile):
     directly when it can, into the workspace otherwise)."""
     width = -(-k // tile) * tile + n
     assert _native.library().ct_parameter_gradients_workspace(m, n, k, r) == r * width * F32
+
+
+@pytest.mark.parametrize("m,decoded_fwd,decoded_dx", [
+    (256, False, False),   # both fused: the packed weight is decoded into LDS tile by tile
+    (384, False, True),    # dx decodes w^T first from 384 rows
+    (511, False, True),
+    (512, True, True),     # the forward from 512
+])
+def test_nf4_decode_first_thresholds(m, decoded_fwd, decoded_dx):
+    """An NF4 weight the entry point decodes first adds its bf16 copy (out x in x 2 bytes)
+    to the workspace query; C5's 6144 -> 24576 projection, rank 256."""
+    lib = _native.library()
+    weight = 24576 * 6144 * 2
+    assert (lib.ct_forward_linear_workspace(m, 24576, 6144, 256, 1) >= weight) == decoded_fwd
+    assert (lib.ct_input_gradient_workspace(m, 24576, 6144, 256, 1) >= weight) == decoded_dx
