@@ -422,7 +422,7 @@ class _Base:
     """The frozen base weight of one projection as the HIP GEMMs consume it.
 
     A packed NF4 weight whose layout the fused loaders accept is handed to the entry points
-    packed: below 512 rows (384 for dx) every GEMM decodes it tile by tile into LDS, from
+    packed: below 512 rows (257 for dx) every GEMM decodes it tile by tile into LDS, from
     there on the entry point decodes it once into its workspace (both bit-identical to
     `materialize`).
     Anything else is materialised here once, as the reference does (linear.py:70,107).

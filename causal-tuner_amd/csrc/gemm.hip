@@ -1687,12 +1687,13 @@ namespace ct {
 namespace {
 // dx decodes its weight first from fewer rows than the forward: its loader, which decodes
 // the packed weight into the transposed layout, is the slower of the two fused loaders,
-// and from 384 rows the transposed decode plus the dense kernel is faster (measured on
-// MI355X at C5's shapes: 384 rows 318 -> 284 and 454 -> 305 us, 511 rows 330 -> 298 and
-// 466 -> 313 us; at 256 rows the fused loader stays faster, 198 against 233 us). The
-// forward's fused loader keeps up to kMaterializeRows (at 384-511 rows the two orders
-// are within 7% either way). Both orders give the same results.
-constexpr int64_t kMaterializeRowsDx = 384;
+// and once the rows need a second 256-row tile (which decodes every weight slice again)
+// the transposed decode plus the dense kernel is faster (measured on MI355X at C5's
+// shapes: 257 rows 314 -> 275 and 454 -> 290 us, 384 rows 318 -> 284 and 454 -> 305 us;
+// at 256 rows the fused loader stays faster, 198 against 233 us). The forward's fused
+// loader keeps up to kMaterializeRows (from 257 rows the two orders are within 7% either
+// way, one shape each). Both orders give the same results.
+constexpr int64_t kMaterializeRowsDx = 257;
 // Also decoded first: a weight without double quantization (the fast runner's NF4 loader
 // needs the nested state) in a problem that splits its reduction, so that it takes the
 // same kernel and summation order as the bf16 weight it decodes to.

@@ -349,7 +349,8 @@ int ct_forward_linear_static(const void *x, int64_t ldx,
  * (lddx), low bf16 [m, r] contiguous. `epilogue` (may be null, needs add = 0) is an
  * elementwise step on dx (ct_epilogue: CT_EPI_DSILU for the MLP's down projection).
  * Workspace query and row regimes as for ct_forward_linear, except that an NF4 weight is
- * decoded first (transposed, [k, n]) from 384 rows on instead of 512.
+ * decoded first (transposed, [k, n]) from 257 rows on (more than one 256-row tile)
+ * instead of 512.
  */
 int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, int64_t r, int32_t nf4);
 int ct_input_gradient(const void *dy, int64_t lddy,

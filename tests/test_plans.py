@@ -95,7 +95,8 @@ def test_parameter_gradients_unsplit(m, n, k, r, tile):
 
 @pytest.mark.parametrize("m,decoded_fwd,decoded_dx", [
     (256, False, False),   # both fused: the packed weight is decoded into LDS tile by tile
-    (384, False, True),    # dx decodes w^T first from 384 rows
+    (257, False, True),    # dx decodes w^T first once a second 256-row tile is needed
+    (384, False, True),
     (511, False, True),
     (512, True, True),     # the forward from 512
 ])
