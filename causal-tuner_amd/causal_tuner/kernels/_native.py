@@ -18,6 +18,7 @@ DEFAULT_LIBRARY = os.path.normpath(os.path.join(_HERE, "..", "..", "lib", "libca
 CT_F32, CT_F16, CT_BF16 = 0, 1, 2
 CT_CAST_MAX = 16  # tensors per ct_cast_f32_bf16 call (include/causal_tuner_hip.h)
 CT_STATIC_SCRATCH_BYTES = 64 << 20  # scratch of ct_forward_linear_static per GPU
+CT_GROUP_MAX = 8  # projections per ct_group_input_gradient call
 CT_PROF_FWD_GEMM, CT_PROF_DX_GEMM, CT_PROF_DEQUANT, CT_PROF_PARAM, CT_PROF_LOWRANK = 1, 2, 4, 8, 16
 DTYPE_CODES = {torch.float32: CT_F32, torch.float16: CT_F16, torch.bfloat16: CT_BF16}
 
@@ -53,6 +54,7 @@ _EPI = ctypes.POINTER(Epilogue)
 
 _SIGNATURES = {
     "ct_abi_version": (ctypes.c_int, []),
+    "ct_init_device": (ctypes.c_int, []),
     "ct_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "ct_nf4_dequant": (ctypes.c_int, [ctypes.POINTER(NF4Weight), _P, _I32, _P]),
     "ct_nf4_fused_supported": (ctypes.c_int, [ctypes.POINTER(NF4Weight)]),
@@ -73,7 +75,13 @@ _SIGNATURES = {
                                               _I64, _I32, _P, _I64, _P]),
     "ct_accumulate_workspace": (_I64, [_I64, _I64, _I64]),
     "ct_silu_multiply": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P]),
-    "ct_rope": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P]),
+    "ct_rope": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P]),
+    "ct_group_forward_workspace": (_I64, [_I64, _I32, _P, _I64, _I64]),
+    "ct_group_forward": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _I64,
+                                        _P]),
+    "ct_group_input_gradient_workspace": (_I64, [_I64, _I32, _P, _P, _I64]),
+    "ct_group_input_gradient": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I64,
+                                               _I64, _I32, _P, _I64, _P]),
     "ct_nf4_quantize_workspace": (_I64, [_I64, _I32, _I32]),
     "ct_nf4_quantize": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "ct_quantize_blockwise": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _P]),
@@ -99,7 +107,7 @@ EXPORTED = tuple(_SIGNATURES)
 _library = None
 
 
-ABI_VERSION = 10   # ct_abi_version() of the library these signatures describe
+ABI_VERSION = 11   # ct_abi_version() of the library these signatures describe
 
 
 def library_path():
@@ -142,10 +150,23 @@ def stream_of(tensor):
     return torch.cuda.current_stream(tensor.device).cuda_stream
 
 
+_READY = set()
+
+
+def _init_device(index):
+    """The library's per-device set-up (ct_init_device), once per GPU with it current."""
+    with torch.cuda.device(index):
+        check(library().ct_init_device(), "ct_init_device")
+    _READY.add(index)
+
+
 def device_of(tensor):
     """A context making the tensor's device current for a launch: a no-op when it already is
-    (the usual single-device case costs one device query instead of two device switches)."""
+    (the usual single-device case costs one device query instead of two device switches).
+    The first launch on a device runs the library's set-up for it."""
     index = tensor.device.index
+    if index not in _READY:
+        _init_device(index)
     if index == torch.cuda.current_device():
         return _CURRENT
     return torch.cuda.device(index)
@@ -191,6 +212,9 @@ def epilogue(kind, rows, in0=None, in1=None, out0=None, out1=None, rotary=None):
             setattr(e, "ld_" + name, ld)
     if rotary is not None:
         cosine, sine, head_dim = rotary
+        if not (cosine.is_contiguous() and sine.is_contiguous() and cosine.dtype == sine.dtype
+                and cosine.shape == sine.shape and cosine.shape[0] == rows):
+            raise ValueError("rotary tables must be contiguous [rows, half] tensors of one dtype")
         e.cosine, e.sine = cosine.data_ptr(), sine.data_ptr()
         e.trig_dtype = dtype_code(cosine.dtype)
         e.head_dim, e.half = int(head_dim), int(cosine.shape[-1])

@@ -66,11 +66,23 @@ class RMS(torch.autograd.Function):
         return (result, dw, None, None, None)[:len(ctx.needs_input_grad)]
 
 
+def _token_pitch(t, tokens, width):
+    """Elements between consecutive tokens of t viewed as [tokens, width] (contiguous within
+    a token), or None when t has no such view."""
+    if t.is_contiguous():
+        return width
+    if t.dim() == 2 and t.shape[0] == tokens and t.shape[1] == width and t.stride(1) == 1 and t.stride(0) >= width:
+        return t.stride(0)
+    return None
+
+
 def _rope(x, y, cosine, sine, head_dim, *, inverse, rotated_only):
-    """y <- RoPE(x) over [tokens, heads, head_dim] with cosine/sine [tokens, half]."""
+    """y <- RoPE(x) over [tokens, heads, head_dim] with cosine/sine [tokens, half]; x and y
+    are contiguous, or [tokens, heads * head_dim] matrices with a row pitch (column ranges of
+    wider matrices)."""
     if not (x.is_cuda and y.is_cuda and cosine.is_cuda and sine.is_cuda):
         raise ValueError("RoPE kernels expect device tensors")
-    if not (x.is_contiguous() and y.is_contiguous() and cosine.is_contiguous() and sine.is_contiguous()):
+    if not (cosine.is_contiguous() and sine.is_contiguous()):
         raise ValueError("RoPE kernels expect contiguous tensors")
     if x.dtype != y.dtype or cosine.dtype != sine.dtype:
         raise ValueError("RoPE: mismatched element types")
@@ -86,10 +98,14 @@ def _rope(x, y, cosine, sine, head_dim, *, inverse, rotated_only):
         tokens, heads = 1, x.numel() // head_dim
     if x.numel() == 0:
         return y
+    width = heads * head_dim
+    ldx, ldy = _token_pitch(x, tokens, width), _token_pitch(y, tokens, width)
+    if ldx is None or ldy is None:
+        raise ValueError("RoPE kernels expect contiguous tensors")
     with _native.device_of(x):
         status = _native.library().ct_rope(
             _native.ptr(x), _native.ptr(y), _native.ptr(cosine), _native.ptr(sine), tokens, heads, head_dim, half,
-            int(inverse), int(rotated_only), _native.dtype_code(x.dtype), _native.dtype_code(cosine.dtype),
+            ldx, ldy, int(inverse), int(rotated_only), _native.dtype_code(x.dtype), _native.dtype_code(cosine.dtype),
             _native.stream_of(x))
     _native.check(status, "ct_rope")
     return y

@@ -14,10 +14,12 @@ lib/libcausal_tuner_hip.so:
   outputs with a fixed-order split reduction over tokens (repeated backward is
   bit-identical; add=False ignores the destination's contents).
 
-The bf16 path is the device path. CPU tensors keep the reference's torch semantics (its
-unfused CPU route); device tensors of another compute dtype raise NotImplementedError,
-except in `accumulate`, which keeps the reference's addmm for operands that are not bf16
-(the fp32 projection loss uses it; linear.py:22-24).
+The bf16 path is the benchmarked device path; float32 device operands run the fp32 GEMM
+(`ct_gemm_f32`, `mm_f32`). CPU tensors keep the reference's torch semantics (its unfused
+CPU route); device tensors of another compute dtype raise NotImplementedError, except in
+`accumulate`, which casts mixed operands to the output dtype as the reference does
+(linear.py:22-23) and then runs the fp32 or bf16 GEMM (a float16 projection loss with a
+float32 head accumulates that way).
 """
 
 import contextlib
@@ -31,6 +33,9 @@ from . import _native
 
 
 # ----------------------------------------------------------------------------- helpers
+_FLOATS = (torch.float16, torch.bfloat16, torch.float32)
+
+
 def _device_bf16(*tensors):
     return all(t.is_cuda and t.dtype == torch.bfloat16 for t in tensors if t is not None)
 
@@ -268,10 +273,14 @@ def accumulate(output, left, right, *, add=True):
         if target.buffer is not output:
             output.copy_(target.buffer + output if add else target.buffer)
     elif output.is_cuda:
-        if _device_f32(output, left, right):
-            mm_f32(left, right, output, add=add)
+        if output.dtype == torch.float32 and left.dtype in _FLOATS and right.dtype in _FLOATS:
+            # the reference casts mixed operands to the output dtype first (linear.py:22-23):
+            # fp16 or bf16 operands widen to float32 exactly, then fp32 products and sums
+            mm_f32(left.float(), right.float(), output, add=add)
         elif _device_bf16(output, left, right):
             _mm_bf16(left, right, output, add=add)   # bf16 parameters: one rounding of acc (+ out)
+        elif output.dtype == torch.bfloat16 and left.dtype in _FLOATS and right.dtype in _FLOATS:
+            _mm_bf16(left.to(torch.bfloat16), right.to(torch.bfloat16), output, add=add)
         else:
             _unsupported("accumulate", output, left, right)
     elif output.dtype != left.dtype:
@@ -403,6 +412,108 @@ def parameter_gradients(x, dy, da, db, low, xa, *, add):
                                              _native.ptr(xa), ldxa, _native.ptr(da), _native.ptr(db), m, n, k, r,
                                              int(add), _native.ptr(ws), ws.numel(), _native.stream_of(x))
     _native.check(status, "ct_parameter_gradients")
+
+
+# From this many rows ct_input_gradient decodes an NF4 weight into its workspace before the
+# dense GEMM (the fused transposing loader loses past one 256-row tile); a group's dx then
+# runs as one contraction over the weights decoded side by side (ct_group_input_gradient).
+GROUP_DX_ROWS = 257
+
+
+def _transposable(base):
+    """Whether ct_group_input_gradient takes this base: a packed NF4 weight its transposed
+    decode accepts, or a dense contiguous bf16 matrix."""
+    if base.state is None:
+        return base.matrix is not None and base.matrix.dtype == torch.bfloat16 and base.matrix.is_contiguous()
+    rows, cols = int(base.state.shape[0]), int(base.state.shape[1])
+    return cols % 16 == 0 and rows % 8 == 0 and base.state.blocksize >= 16 and base.weight.data_ptr() % 8 == 0
+
+
+def group_dx_ready(bases, widths, ranks, rows):
+    """Whether the projections' input gradients run as one contraction."""
+    return (1 < len(bases) <= _native.CT_GROUP_MAX and rows >= GROUP_DX_ROWS and all(r > 0 for r in ranks)
+            and all(n % 8 == 0 for n in widths) and all(_transposable(b) for b in bases))
+
+
+def stacked_rows(tensors):
+    """[t_1; t_2; ...] for contiguous matrices of one width: a view when they are consecutive
+    rows of one buffer (the stacked factors group_factors casts into), else a copy."""
+    first = tensors[0]
+    width, offset = first.shape[1], first.data_ptr()
+    for t in tensors:
+        if not t.is_contiguous() or t.shape[1] != width or t.data_ptr() != offset:
+            return torch.cat(tensors)
+        offset += t.numel() * t.element_size()
+    return first.as_strided((sum(len(t) for t in tensors), width), (width, 1))
+
+
+def group_input_gradient(bases, dy, widths, ranks, a_stack, bs, dx, low, add):
+    """low_i = dy_i b_i and dx (+)= sum_i (dy_i w_i + low_i a_i) for projections that read one
+    input (the reference's input_gradient per projection with add=index>0, linear.py:107-122),
+    as one contraction rounded once: ct_group_input_gradient. dy = [dy_1 | dy_2 | ...] and low
+    = [low_1 | low_2 | ...] are column blocks of two matrices."""
+    m, k = dx.shape
+    count = len(bases)
+    dy, lddy = _rows(dy)
+    written, ldlow = _rows(low)
+    if written.data_ptr() != low.data_ptr():
+        raise ValueError("group_input_gradient: low must be a 16-byte aligned matrix with unit row stride")
+    target = _Output(dx)
+    if add and target.buffer is not dx:
+        target.buffer.copy_(dx)
+    descs = [None if base.state is None else _native.nf4_descriptor(base.weight, base.state) for base in bases]
+    dense = (ctypes.c_void_p * count)(*[None if d is not None else base.matrix.data_ptr()
+                                        for base, d in zip(bases, descs)])
+    packed = (ctypes.POINTER(_native.NF4Weight) * count)(*[None if d is None else ctypes.pointer(d) for d in descs])
+    factors = (ctypes.c_void_p * count)(*[b.contiguous().data_ptr() for b in bs])
+    n_arr, r_arr = (ctypes.c_int64 * count)(*widths), (ctypes.c_int64 * count)(*ranks)
+    lib = _native.library()
+    ws = _workspace(lib.ct_group_input_gradient_workspace(m, count, n_arr, r_arr, k), dx.device)
+    with _native.device_of(dx):
+        status = lib.ct_group_input_gradient(
+            _native.ptr(dy), lddy, count, n_arr, r_arr, dense, packed, _native.ptr(a_stack.contiguous()), factors,
+            _native.ptr(target.buffer), target.ld, _native.ptr(low), ldlow, m, k, int(add), _native.ptr(ws),
+            ws.numel(), _native.stream_of(dx))
+    _native.check(status, "ct_group_input_gradient")
+    target.finish()
+
+
+# From this many rows ct_forward_linear decodes an NF4 weight before its dense GEMM; two
+# projections that share an input then run their forward as one GEMM (ct_group_forward).
+GROUP_FORWARD_ROWS = 512
+
+
+def group_forward_ready(bases, widths, ranks, rows, k, biases):
+    return (len(bases) == 2 and rows >= GROUP_FORWARD_ROWS and ranks[0] == ranks[1] > 0 and widths[0] % 256 == 0
+            and k % 8 == 0 and all(b is None for b in biases)
+            and all(base.state is not None or (base.matrix.dtype == torch.bfloat16 and base.matrix.is_contiguous())
+                    for base in bases))
+
+
+def group_forward(bases, x, b_stack, xa, outputs):
+    """out_i = x w_i^T + xa_i b_i^T for two projections that read x (forward_linear with the
+    stacked xa given, linear.py:72-86) as one GEMM over [w_1; w_2]: ct_group_forward. xa =
+    [xa_1 | xa_2]; `outputs` are written in place."""
+    m, k = x.shape
+    x, ldx = _rows(x)
+    xa, ldxa = _rows(xa)
+    targets = [_Output(out) for out in outputs]
+    descs = [None if base.state is None else _native.nf4_descriptor(base.weight, base.state) for base in bases]
+    dense = (ctypes.c_void_p * 2)(*[None if d is not None else base.matrix.data_ptr() for base, d in zip(bases, descs)])
+    packed = (ctypes.POINTER(_native.NF4Weight) * 2)(*[None if d is None else ctypes.pointer(d) for d in descs])
+    n_arr = (ctypes.c_int64 * 2)(*[out.shape[1] for out in outputs])
+    out_arr = (ctypes.c_void_p * 2)(*[t.buffer.data_ptr() for t in targets])
+    ld_arr = (ctypes.c_int64 * 2)(*[t.ld for t in targets])
+    r = b_stack.shape[1]
+    lib = _native.library()
+    ws = _workspace(lib.ct_group_forward_workspace(m, 2, n_arr, k, r), x.device)
+    with _native.device_of(x):
+        status = lib.ct_group_forward(_native.ptr(x), ldx, 2, n_arr, dense, packed, _native.ptr(b_stack.contiguous()),
+                                      _native.ptr(xa), ldxa, out_arr, ld_arr, m, k, r, _native.ptr(ws), ws.numel(),
+                                      _native.stream_of(x))
+    _native.check(status, "ct_group_forward")
+    for t in targets:
+        t.finish()
 
 
 def projection_parameters(module):
@@ -541,16 +652,29 @@ class _LoRAGroup(torch.autograd.Function):
             half = cosine.shape[-1]
             trig = tuple(value.reshape(-1, half) if value.numel() == len(flat) * half else None
                          for value in (cosine, sine))
+        # the fused step reads [rows, half] tables with a row pitch of half and one dtype;
+        # anything else takes the separate pass, which validates the tables itself
         rope_fused = bool(rotated) and trig[0] is not None and trig[1] is not None and \
+            trig[0].is_contiguous() and trig[1].is_contiguous() and trig[0].dtype == trig[1].dtype and \
             fusable(*outputs[:rotated]) and all(out.shape[1] % head_dim == 0 for out in outputs[:rotated])
         residual_flat = None if residual is None else residual.reshape(len(flat), -1)
         residual_fused = residual_flat is not None and not rotated and fusable(outputs[0], residual_flat)
+        # Two projections of one rank without biases or steps (gate and up) share one grid of
+        # output tiles from GROUP_FORWARD_ROWS rows: one partial last round instead of two.
+        paired = (stack is not None and not rotated and residual is None and x.is_cuda and dtype == torch.bfloat16
+                  and group_forward_ready(bases, [out.shape[1] for out in outputs], ranks, span, flat.shape[1],
+                                          biases))
+        if paired:
+            b_stack = stacked_rows([factors[1], factors[3]])
         for start in range(0, len(flat), step):
             part = flat[start:start+step]
             rows = slice(start, start+len(part)) if keep else slice(0, len(part))
             window = slice(start, start+len(part))
             if stack is not None:
                 _low_rank(part, stack, xa[rows], transpose=True)
+            if paired and len(part) > 64:
+                group_forward(bases, part, b_stack, xa[rows], [out[window] for out in outputs])
+                continue
             for index, base in enumerate(bases):
                 epilogue = None
                 if rope_fused and index < rotated:
@@ -595,11 +719,30 @@ class _LoRAGroup(torch.autograd.Function):
         signals = [grad.reshape(-1, grad.shape[-1]).to(ctx.dtype) for grad in grad_outputs]
         allocate = torch.empty_like if len(flat) else torch.zeros_like
         gradients = [(allocate(parameters[4*i+1]), allocate(parameters[4*i+2])) for i in range(count)]
-        low = torch.empty((span, max(ranks)), device=x.device, dtype=ctx.dtype)
         xa = None if kept else torch.empty((span, sum(ranks)), device=x.device, dtype=ctx.dtype)
         rotated = min(count, 2) if ctx.head_dim else 0
+        widths = [signal.shape[1] for signal in signals]
+        # From GROUP_DX_ROWS rows the group's input gradient is one contraction over the
+        # upstream gradients side by side (the q/k ones rotated back into their columns)
+        # and the weights decoded side by side: dx is rounded once instead of after every
+        # projection, and k and v add no pass over dx.
+        # The upstream gradients arrive as separate tensors: the ones not rotated on the way
+        # in are copied side by side, which pays only while the copies move fewer bytes than
+        # the dx passes the one contraction saves (one read and write of dx per projection
+        # after the first): q/k/v, not two wide projections such as gate and up.
+        copied = sum(widths[rotated:])
+        grouped = (dx is not None and x.is_cuda and ctx.dtype == torch.bfloat16
+                   and group_dx_ready(bases, widths, ranks, span) and copied < (count - 1) * flat.shape[1])
+        if grouped:
+            joined = torch.empty((span, sum(widths)), device=x.device, dtype=ctx.dtype)
+            low = torch.empty((span, sum(ranks)), device=x.device, dtype=ctx.dtype)
+            a_stack = stack if stack is not None else stacked_rows([factors[2*i] for i in range(count)])
+            columns = [slice(sum(widths[:i]), sum(widths[:i+1])) for i in range(count)]
+            low_columns = [slice(sum(ranks[:i]), sum(ranks[:i+1])) for i in range(count)]
+        else:
+            low = torch.empty((span, max(ranks)), device=x.device, dtype=ctx.dtype)
         scratch = (torch.empty(span * max(signals[i].shape[1] for i in range(rotated)), device=x.device,
-                               dtype=ctx.dtype) if rotated else None)
+                               dtype=ctx.dtype) if rotated and not grouped else None)
         for start in range(0, len(flat), step):
             part = flat[start:start+step]
             if not kept:
@@ -607,8 +750,30 @@ class _LoRAGroup(torch.autograd.Function):
                     _low_rank(part, stack, xa[:len(part)], transpose=True)
                 else:
                     for index in range(count):
-                        columns = slice(sum(ranks[:index]), sum(ranks[:index+1]))
-                        _low_rank(part, factors[2*index], xa[:len(part), columns], transpose=True)
+                        columns_xa = slice(sum(ranks[:index]), sum(ranks[:index+1]))
+                        _low_rank(part, factors[2*index], xa[:len(part), columns_xa], transpose=True)
+            if grouped:
+                tile_signals = []
+                for index in range(count):
+                    signal = signals[index][start:start+len(part)]
+                    target = joined[:len(part), columns[index]]
+                    if index < rotated:
+                        from .core_cuda import inverse_rope_tile
+                        signal = inverse_rope_tile(signal, cosine[start:start+len(part)],
+                                                   sine[start:start+len(part)], ctx.head_dim, target)
+                    else:
+                        target.copy_(signal)
+                        signal = target
+                    tile_signals.append(signal)
+                group_input_gradient(bases, joined[:len(part)], widths, ranks, a_stack,
+                                     [factors[2*i+1] for i in range(count)], dx[start:start+len(part)],
+                                     low[:len(part)], False)
+                for index in range(count):
+                    inputs = (kept[index][start:start+len(part)] if kept else
+                              xa[:len(part), sum(ranks[:index]):sum(ranks[:index+1])])
+                    parameter_gradients(part, tile_signals[index], *gradients[index],
+                                        low[:len(part), low_columns[index]], inputs, add=start > 0)
+                continue
             for index in range(count):
                 a, b = factors[2*index], factors[2*index+1]
                 signal = signals[index][start:start+len(part)]

@@ -26,8 +26,8 @@ results into separate tile buffers so the kept values survive a repeated backwar
 import torch
 
 from . import _native
-from .linear import _Base, _low_rank, forward_linear, fusable, group_factors, input_gradient, parameter_gradients, \
-    projection_parameters
+from .linear import _Base, _low_rank, forward_linear, fusable, group_dx_ready, group_factors, group_input_gradient, \
+    input_gradient, parameter_gradients, projection_parameters, stacked_rows
 
 
 # ----------------------------------------------------------------------------- SiLU x up
@@ -204,8 +204,19 @@ def _backward(ctx, grad, x, kept, parameters):
     fresh = torch.empty_like if rows else torch.zeros_like
     grads = [(fresh(parameters[4 * i + 1]), fresh(parameters[4 * i + 2])) for i in range(3)]
     span = min(tile, rows)
+    # From GROUP_DX_ROWS rows gate's and up's input gradients are one contraction over
+    # [d gate | d up]: the two tile buffers are then the column halves of one matrix.
+    grouped = (dx is not None and flat.is_cuda and dtype == torch.bfloat16
+               and group_dx_ready(mlp.bases[:2], [mlp.width] * 2, mlp.rank[:2], span))
     # three [tile, width] buffers: (gate, up, dh) in, (d gate, d up, h) out
-    first, second, third = (mlp.empty(span, mlp.width) for _ in range(3))
+    if grouped:
+        joined = mlp.empty(span, 2 * mlp.width)
+        first, second = joined[:, :mlp.width], joined[:, mlp.width:]
+        third = mlp.empty(span, mlp.width)
+        low_pair = mlp.empty(span, mlp.rank[GATE] + mlp.rank[UP])
+        a_stack = mlp.stacked if mlp.stacked is not None else stacked_rows(mlp.a[:2])
+    else:
+        first, second, third = (mlp.empty(span, mlp.width) for _ in range(3))
     low = mlp.empty(span, max(mlp.rank))
     xa_down = mlp.empty(span, mlp.rank[DOWN])
     pair_tile, xa_tile = (None, None) if kept else mlp.xa_buffer(span)
@@ -228,11 +239,25 @@ def _backward(ctx, grad, x, kept, parameters):
         dsilu = (_native.epilogue(_native.CT_EPI_DSILU, n, in0=gate, in1=up, out0=d_gate, out1=d_up) if fused
                  else None)
         mlp.input_gradient(DOWN, dy, d_hidden, low[:n, :mlp.rank[DOWN]], False, dsilu)
-        if not fused:
+        if not fused and grouped:
+            # the separate kernel takes contiguous operands: column halves go through copies
+            g, u = gate.contiguous(), up.contiguous()
+            dg, du = torch.empty_like(g), torch.empty_like(u)
+            _silu_kernel(g, u, d_hidden, dg, du, backward=True, reconstruct=True)
+            d_gate.copy_(dg)
+            d_up.copy_(du)
+        elif not fused:
             _silu_kernel(gate, up, d_hidden, d_gate, d_up, backward=True, reconstruct=True)
         hidden = d_hidden
         _low_rank(hidden, mlp.a[DOWN], xa_down[:n], transpose=True)
         parameter_gradients(hidden, dy, *grads[DOWN], low[:n, :mlp.rank[DOWN]], xa_down[:n], add=start > 0)
+        if grouped:
+            group_input_gradient(mlp.bases[:2], joined[:n], [mlp.width] * 2, mlp.rank[:2], a_stack, mlp.b[:2],
+                                 dx[window], low_pair[:n], False)
+            for which, signal, columns in ((GATE, d_gate, slice(0, mlp.rank[GATE])),
+                                           (UP, d_up, slice(mlp.rank[GATE], mlp.rank[GATE] + mlp.rank[UP]))):
+                parameter_gradients(part, signal, *grads[which], low_pair[:n, columns], xa[which], add=start > 0)
+            continue
         for which, signal in ((GATE, d_gate), (UP, d_up)):
             grad_low = low[:n, :mlp.rank[which]]
             if dx is not None:

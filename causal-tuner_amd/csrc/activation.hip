@@ -112,6 +112,19 @@ hipError_t launch(const void *gate, const void *up, void *h, void *dg, void *du,
 }
 
 }  // namespace
+
+// h = bf16(silu(gate)) * up over n contiguous bf16 elements with silu_multiply_vec: the
+// pass after a GEMM whose SiLU step runs outside it (the product in `up`), with the kernel
+// and the bits of ct_silu_multiply. Needs n % 8 == 0 and 16-byte aligned operands.
+hipError_t silu_forward_flat(const uint16_t *gate, const uint16_t *up, uint16_t *h, int64_t n, hipStream_t s) {
+    if (n % 8 || !aligned16(gate) || !aligned16(up) || !aligned16(h)) return hipErrorInvalidValue;
+    const int64_t chunks = n / 8;
+    silu_multiply_vec<false, true><<<dim3((unsigned)cdiv(chunks, 256)), dim3(256), 0, s>>>(
+        reinterpret_cast<const uint4 *>(gate), reinterpret_cast<const uint4 *>(up), reinterpret_cast<uint4 *>(h),
+        nullptr, nullptr, chunks);
+    return hipGetLastError();
+}
+
 }  // namespace ct
 
 extern "C" int ct_silu_multiply(const void *gate, const void *up, void *h, void *dgate, void *dup, int64_t n,

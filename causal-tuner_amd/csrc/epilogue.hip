@@ -41,11 +41,18 @@ hipError_t launch_rows(const EpiParams &e, const uint16_t *src, int64_t ldsrc, u
 
 }  // namespace
 
+hipError_t silu_forward_flat(const uint16_t *gate, const uint16_t *up, uint16_t *h, int64_t n, hipStream_t s);
+
 hipError_t epilogue_run(const EpiParams &e, const uint16_t *src, int64_t ldsrc, uint16_t *dst, int64_t lddst, int64_t m,
                         int64_t n, hipStream_t stream) {
     if (e.kind == CT_EPI_NONE || m <= 0 || n <= 0) return hipSuccess;
     const bool vec = reinterpret_cast<uintptr_t>(src) % 16 == 0 && ldsrc % 8 == 0 &&
                      reinterpret_cast<uintptr_t>(dst) % 16 == 0 && lddst % 8 == 0;
+    // A SiLU step over whole contiguous matrices runs ct_silu_multiply's kernel (the same
+    // per-element code): measured on MI355X, the row kernel below ran it slower than that.
+    if (e.kind == CT_EPI_SILU && !e.out0 && vec && e.vec && ldsrc == n && lddst == n && e.ld_in0 == n &&
+        (m * n) % 8 == 0)
+        return silu_forward_flat(e.in0, src, dst, m * n, stream);
     switch (e.kind) {
         case CT_EPI_RESIDUAL: return launch_rows<CT_EPI_RESIDUAL>(e, src, ldsrc, dst, lddst, m, n, vec, stream);
         case CT_EPI_SILU: return launch_rows<CT_EPI_SILU>(e, src, ldsrc, dst, lddst, m, n, vec, stream);

@@ -27,7 +27,8 @@
 // reads (ds_read_b128) and the loader writes are free of bank conflicts. Tiles are double
 // buffered: the next tile's global loads are in flight while the current one feeds MFMA.
 //
-// Tile shapes: 256x256 (4 waves of 128x128, accumulators in AGPRs), 128x128 and 64x64.
+// Tile shapes: 256x256 (gemm_big8: 8 waves of 64x128, two per SIMD; the generic runner's
+// gemm_big: 4 waves of 128x128), 128x128 and 64x64 (4 waves).
 // Workgroup ids are remapped so each of the 8 XCDs walks a contiguous, M-grouped range of
 // output tiles: the workgroups that share an L2 also share A and B panels.
 
@@ -40,7 +41,7 @@ namespace ct {
 
 int validate_nf4(const ct_nf4_weight *w);
 bool nf4_transposable(const ct_nf4_weight *w);
-hipError_t nf4_dequant_transposed(const ct_nf4_weight *w, void *out, hipStream_t stream);
+hipError_t nf4_dequant_transposed(const ct_nf4_weight *w, void *out, hipStream_t stream, int64_t ldo = 0);
 
 namespace {
 
@@ -789,7 +790,23 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     else sg0 = p.seg[0];
     const int64_t n0 = (int64_t)(second ? tn - p.group_tiles : tn) * BN;
     const int64_t ncols = second ? p.n1 : p.n;
-    const int64_t out_shift = second ? (int64_t)p.group_tiles * BN : 0;
+    // The second of two side-by-side projections (ct_group_forward): its own output matrix
+    // and its columns of the stacked xa. Chosen by branches on the uniform condition (see
+    // sg0 above).
+    const bool alt = p.alt_col > 0 && n0 >= p.alt_col;
+    void *cout = p.c;
+    int64_t ldc = p.ldc;
+    int64_t out_shift = second ? (int64_t)p.group_tiles * BN : 0;
+    Segment sg1;
+    if (alt) {
+        sg1 = p.seg[1];
+        sg1.a.p = static_cast<const uint16_t *>(sg1.a.p) + p.alt_a1;
+        cout = p.c_alt;
+        ldc = p.ldc_alt;
+        out_shift = -p.alt_col;
+    } else {
+        sg1 = p.seg[1];
+    }
 
     if constexpr (kNF4) {
         if (tid < 16) lcode[tid] = p.code[tid];
@@ -819,10 +836,10 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     if (t1 > 0) {
         const int64_t b = tbeg > t0 ? tbeg - t0 : 0, e = tend - t0;
         if constexpr (MODE == 2)
-            FastRunner<BM, BN, A1, B1, WAVES_M, WAVES_N>::run(p.seg[1], p.m, p.n, m0, n0, b, e, acc, lds0, lds1,
+            FastRunner<BM, BN, A1, B1, WAVES_M, WAVES_N>::run(sg1, p.m, p.n, m0, n0, b, e, acc, lds0, lds1,
                                                               lcode, lcode2, tid, wm0, wn0);
         else
-            SegmentRunner<BM, BN, A1, B1, VEC>::run(p.seg[1], p.m, p.n, m0, n0, b, e, acc, lds0, lds1, lcode,
+            SegmentRunner<BM, BN, A1, B1, VEC>::run(sg1, p.m, p.n, m0, n0, b, e, acc, lds0, lds1, lcode,
                                                     lcode2, tid, wm0, wn0);
     }
 
@@ -916,7 +933,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) v[j] = acc[i][j][e] + bias[j];
             if constexpr (OUT == CT_F32) {
-                float *c = static_cast<float *>(p.c) + (int64_t)blockIdx.z * p.split_stride + row * p.ldc +
+                float *c = static_cast<float *>(cout) + (int64_t)blockIdx.z * p.split_stride + row * ldc +
                            out_shift + col;
                 if (VEC && full && FN % 4 == 0) {
 #pragma unroll
@@ -933,7 +950,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
                     }
                 }
             } else {
-                uint16_t *c = static_cast<uint16_t *>(p.c) + row * p.ldc + out_shift + col;
+                uint16_t *c = static_cast<uint16_t *>(cout) + row * ldc + out_shift + col;
                 if (p.beta) {
                     if (VEC && full && (FN == 8 || FN == 4)) {
                         // one 16- or 8-byte read of the FN existing values
@@ -1025,10 +1042,15 @@ __global__ __launch_bounds__(256) void reduce_splits(const float *__restrict__ w
 // reduce_splits with 16-byte accesses, eight columns per thread, the same sums in the same
 // order (identical results). Needs cols % 8 == 0, 16-byte aligned partials, output and
 // bias, and ldo % 8 == 0. Grid: (column blocks of 2048, rows).
+// With `res` (bf16 output only, add = 0): the residual step of the projection epilogue,
+// out = bf16(bf16(sum) + res), the reference's add_ on the stored output
+// (kernels/linear.py:90-91, kernels/mlp_cuda.py:80), fused into the reduction.
 template <int OUT>
 __global__ __launch_bounds__(256) void reduce_splits_vec(const float *__restrict__ ws, int splits, int64_t stride,
                                                          int64_t rows, int64_t cols, void *out, int64_t ldo, int add,
-                                                         const uint16_t *__restrict__ bias) {
+                                                         const uint16_t *__restrict__ bias,
+                                                         const uint16_t *__restrict__ res = nullptr,
+                                                         int64_t ldres = 0) {
     const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8, r = blockIdx.y;
     if (c >= cols) return;
     const float *src = ws + r * cols + c;
@@ -1074,6 +1096,13 @@ __global__ __launch_bounds__(256) void reduce_splits_vec(const float *__restrict
             const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) s[e] = s[e] + bf16_to_f32((uint16_t)(w[e / 2] >> (16 * (e & 1))));
+        }
+        if (res) {
+            const uint4 q = *reinterpret_cast<const uint4 *>(res + r * ldres + c);
+            const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                s[e] = bf16_to_f32(bf16_bits(s[e])) + bf16_to_f32((uint16_t)(w[e / 2] >> (16 * (e & 1))));
         }
         *o = make_uint4(pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3]), pack_bf16x2(s[4], s[5]),
                         pack_bf16x2(s[6], s[7]));
@@ -1341,12 +1370,18 @@ int64_t total_tiles(const GemmParams &p) {
 
 // out (+)= sum of the fp32 split partials in ws (+ bias), in split order: 16-byte accesses
 // where the layout allows them (the same sums either way).
+bool reduce_vec_ok(const float *ws, int64_t cols, const void *out, int64_t ldo, const uint16_t *bias) {
+    return cols % 8 == 0 && ldo % 8 == 0 && aligned16(ws) && aligned16(out) && (!bias || aligned16(bias));
+}
+
 template <int OUT>
 hipError_t launch_reduce(const float *ws, int splits, int64_t stride, int64_t rows, int64_t cols, void *out,
-                         int64_t ldo, int add, const uint16_t *bias, hipStream_t s) {
-    if (cols % 8 == 0 && ldo % 8 == 0 && aligned16(ws) && aligned16(out) && (!bias || aligned16(bias)))
+                         int64_t ldo, int add, const uint16_t *bias, hipStream_t s, const uint16_t *res = nullptr,
+                         int64_t ldres = 0) {
+    if (res && !reduce_vec_ok(ws, cols, out, ldo, bias)) return hipErrorInvalidValue;
+    if (reduce_vec_ok(ws, cols, out, ldo, bias))
         reduce_splits_vec<OUT><<<dim3((unsigned)cdiv(cols, 2048), (unsigned)rows), 256, 0, s>>>(
-            ws, splits, stride, rows, cols, out, ldo, add, bias);
+            ws, splits, stride, rows, cols, out, ldo, add, bias, res, ldres);
     else
         reduce_splits<OUT><<<dim3((unsigned)cdiv(cols, 256), (unsigned)rows), 256, 0, s>>>(ws, splits, stride, rows,
                                                                                           cols, out, ldo, add, bias);
@@ -1371,8 +1406,18 @@ int mid_split_route(const Problem &pr) {
 // units idle, after every tile at once (measured slower than the separate pass at 4096 x
 // 8192), while the 128 x 128 tiles run two workgroups per CU and overlap one's step with
 // the other's products.
+// The residual step on the split route rides in the split reduction (reduce_splits_vec),
+// which reads the partials and writes the output anyway: measured on MI355X, the pass after
+// the reduction cost more than a separate add (C4's down projection, 4096 x 2048 over 8448).
+bool residual_in_reduction(const Problem &pr) {
+    const GemmParams &p = pr.p;
+    return p.epi.kind == CT_EPI_RESIDUAL && !p.beta && p.epi.vec && p.epi.in0 && mid_split_route(pr) > 1 &&
+           aligned16(p.c) && p.ldc % 8 == 0 && (!p.bias || aligned16(p.bias));
+}
+
 bool epilogue_fused(const Problem &pr) {
     const GemmParams &p = pr.p;
+    if (residual_in_reduction(pr)) return true;
     if (mid_split_route(pr) > 1) return false;
     if (pr.splits == 1 && pr.out == CT_BF16 && p.m <= 64) {
         const int sa[2] = {pr.src[0], p.nseg > 1 ? pr.src[2] : pr.src[0]};
@@ -1429,10 +1474,12 @@ hipError_t run(Problem &pr, hipStream_t s) {
         q.p.split_stride = p.m * p.n;
         q.p.beta = 0;
         q.p.bias = nullptr;
+        q.p.epi.kind = CT_EPI_NONE;  // a residual step is applied by the reduction below
         const hipError_t e = run(q, s);
         if (e != hipSuccess) return e;
+        const bool res = p.epi.kind == CT_EPI_RESIDUAL;
         return launch_reduce<CT_BF16>(static_cast<const float *>(pr.ws), splits, p.m * p.n, p.m, p.n, p.c, p.ldc,
-                                      p.beta, p.bias, s);
+                                      p.beta, p.bias, s, res ? p.epi.in0 : nullptr, res ? p.epi.ld_in0 : 0);
     }
     if (pr.splits == 1 && pr.out == CT_BF16 && p.m <= 64) {
         // Few rows: the workgroup streams the weight with its 8 waves splitting the reduction.
@@ -1602,7 +1649,7 @@ bool nf4_fusable(const ct_nf4_weight *w) {
 
 using namespace ct;
 
-extern "C" int ct_abi_version(void) { return 10; }
+extern "C" int ct_abi_version(void) { return 11; }
 
 extern "C" const char *ct_status_string(int status) {
     switch (status) {
@@ -1862,6 +1909,78 @@ extern "C" int ct_forward_linear(const void *x, int64_t ldx, const void *w_dense
     return to_status(e);
 }
 
+extern "C" int64_t ct_group_forward_workspace(int64_t m, int32_t count, const int64_t *n, int64_t k, int64_t r) {
+    if (m <= 0 || k <= 0 || count != 2 || !n || n[0] <= 0 || n[1] <= 0) return 0;
+    return weight_bytes(n[0] + n[1], k);
+}
+
+extern "C" int ct_group_forward(const void *x, int64_t ldx, int32_t count, const int64_t *n,
+                                const void *const *w_dense, const ct_nf4_weight *const *w_nf4, const void *b_stack,
+                                const void *xa, int64_t ldxa, void *const *out, const int64_t *ldo, int64_t m, int64_t k,
+                                int64_t r, void *workspace, int64_t workspace_bytes, hipStream_t stream) {
+    if (count != 2 || !n || !out || !ldo) return -CT_EINVAL_SHAPE;
+    if (m < 0 || k < 0 || r < 0 || n[0] <= 0 || n[1] <= 0) return -CT_EINVAL_SHAPE;
+    if (m == 0) return 0;
+    // the second projection starts on a tile boundary of every tile size (256)
+    if (n[0] % 256 || k % 8 || (r > 0 && ldxa < 2 * r)) return -CT_EINVAL_SHAPE;
+    if (!x || !out[0] || !out[1] || (r > 0 && (!xa || !b_stack))) return -CT_EINVAL_POINTER;
+    if (ldx < k || ldo[0] < n[0] || ldo[1] < n[1]) return -CT_EINVAL_SHAPE;
+    if (k == 0) return -CT_EINVAL_SHAPE;
+    const int64_t nt = n[0] + n[1];
+    for (int i = 0; i < 2; ++i) {
+        const void *wd = w_dense ? w_dense[i] : nullptr;
+        const ct_nf4_weight *wq = w_nf4 ? w_nf4[i] : nullptr;
+        if (!wd == !wq) return -CT_EINVAL_POINTER;
+        if (wq) {
+            if (const int st = validate_nf4(wq)) return st;
+            if (wq->rows != n[i] || wq->cols != k) return -CT_EINVAL_SHAPE;
+        }
+    }
+    // [w_1; w_2] decoded (or copied) row by row into the workspace: one [n_total, k] operand
+    void *wbuf = nullptr;
+    if (const int st = take_weight(workspace, workspace_bytes, nt, k, wbuf)) return st;
+    for (int i = 0; i < 2; ++i) {
+        uint16_t *dst = static_cast<uint16_t *>(wbuf) + (i ? n[0] * k : 0);
+        if (w_nf4 && w_nf4[i]) {
+            if (const int st = ct_nf4_dequant(w_nf4[i], dst, CT_BF16, stream)) return st;
+        } else {
+            const hipError_t e = hipMemcpyAsync(dst, w_dense[i], (size_t)(n[i] * k * 2), hipMemcpyDeviceToDevice,
+                                                stream);
+            if (e != hipSuccess) return to_status(e);
+        }
+    }
+    Problem pr{};
+    pr.p.seg[0].a = dense(x, ldx);
+    pr.p.seg[0].b = dense(wbuf, k);
+    pr.p.seg[0].k = k;
+    pr.p.seg[1].a = dense(xa, ldxa);
+    pr.p.seg[1].b = dense(b_stack, r);
+    pr.p.seg[1].k = r;
+    pr.p.nseg = r > 0 ? 2 : 1;
+    pr.p.m = m;
+    pr.p.n = nt;
+    pr.p.c = out[0];
+    pr.p.ldc = ldo[0];
+    pr.p.alt_col = n[0];
+    pr.p.alt_a1 = r;
+    pr.p.c_alt = out[1];
+    pr.p.ldc_alt = ldo[1];
+    pr.src[0] = pr.src[1] = pr.src[2] = pr.src[3] = SRC_KC;
+    pr.out = CT_BF16;
+    pr.splits = 1;
+    pr.tile = -1;
+    // The few-row kernels do not take the column switch, and without a workspace the
+    // split route is not taken: the tiled kernels only.
+    if (m <= 64) return -CT_EINVAL_SHAPE;
+    pr.ws = nullptr;
+    pr.ws_bytes = 0;
+    pr.vec = vec_ok(pr) && aligned16(out[1]) && ldo[1] % 8 == 0;
+    const int slot = profile_open(CT_PROF_FWD_GEMM, stream);
+    const hipError_t e = run(pr, stream);
+    profile_close(slot, stream, 2.0 * m * nt * (double)(k + r));
+    return to_status(e);
+}
+
 extern "C" int64_t ct_input_gradient_workspace(int64_t m, int64_t n, int64_t k, int64_t r, int32_t nf4) {
     const int64_t inner = ct_gemm_workspace(m, r, n, 0, 0, CT_BF16);
     const int64_t ks[2] = {n, r};
@@ -1946,6 +2065,136 @@ extern "C" int ct_input_gradient(const void *dy, int64_t lddy, const void *w_den
     const int slot = profile_open(CT_PROF_DX_GEMM, stream);
     const hipError_t e = run(pr, stream);
     profile_close(slot, stream, 2.0 * m * k * (double)(n + r));
+    return to_status(e);
+}
+
+namespace ct {
+namespace {
+// out[c][r] = in[r][c] for a bf16 [rows, cols] matrix (pitches ldin, ldo): 64 x 64 tiles
+// through LDS, the padded row keeping the column reads free of bank conflicts.
+__global__ __launch_bounds__(256) void transpose_bf16(const uint16_t *__restrict__ in, int64_t ldin, int64_t rows,
+                                                      int64_t cols, uint16_t *__restrict__ out, int64_t ldo) {
+    __shared__ uint16_t tile[64][66];
+    const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int i = ty; i < 64; i += 4)
+        if (r0 + i < rows && c0 + tx < cols) tile[i][tx] = in[(r0 + i) * ldin + c0 + tx];
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4)
+        if (c0 + i < cols && r0 + tx < rows) out[(c0 + i) * ldo + r0 + tx] = tile[tx][i];
+}
+
+// Reduction widths of a projection group's dx: n_total (the side-by-side upstream
+// gradients) and r_total (the stacked ranks), or -1 for an invalid description.
+int group_widths(int32_t count, const int64_t *n, const int64_t *r, int64_t *n_total, int64_t *r_total) {
+    if (count < 1 || count > CT_GROUP_MAX || !n || !r) return -1;
+    *n_total = *r_total = 0;
+    for (int i = 0; i < count; ++i) {
+        if (n[i] <= 0 || r[i] < 0) return -1;
+        *n_total += n[i];
+        *r_total += r[i];
+    }
+    return 0;
+}
+}  // namespace
+}  // namespace ct
+
+extern "C" int64_t ct_group_input_gradient_workspace(int64_t m, int32_t count, const int64_t *n, const int64_t *r,
+                                                     int64_t k) {
+    int64_t nt, rt;
+    if (m <= 0 || k <= 0 || group_widths(count, n, r, &nt, &rt)) return 0;
+    int64_t low = 0;
+    for (int i = 0; i < count; ++i) {
+        const int64_t w = r[i] > 0 ? ct_gemm_workspace(m, r[i], n[i], 0, 0, CT_BF16) : 0;
+        low = w > low ? w : low;
+    }
+    const int64_t ks[2] = {nt, rt};
+    const int sb[2] = {SRC_KC, SRC_KS};
+    const int64_t main = problem_workspace(m, k, ks, rt > 0 ? 2 : 1, sb);
+    return weight_bytes(nt, k) + (low > main ? low : main);
+}
+
+extern "C" int ct_group_input_gradient(const void *dy, int64_t lddy, int32_t count, const int64_t *n,
+                                       const int64_t *r, const void *const *w_dense,
+                                       const ct_nf4_weight *const *w_nf4, const void *a_stack, const void *const *b,
+                                       void *dx, int64_t lddx, void *low, int64_t ldlow, int64_t m, int64_t k,
+                                       int32_t add, void *workspace, int64_t workspace_bytes, hipStream_t stream) {
+    int64_t nt, rt;
+    if (m < 0 || k < 0 || group_widths(count, n, r, &nt, &rt)) return -CT_EINVAL_SHAPE;
+    if (m == 0 || k == 0) return 0;
+    if (!dy || !dx || (rt > 0 && (!a_stack || !low || !b))) return -CT_EINVAL_POINTER;
+    if (lddy < nt || lddx < k || (rt > 0 && ldlow < rt)) return -CT_EINVAL_SHAPE;
+    // Every projection's w^T goes side by side into the workspace: [k, n_total], 16-byte
+    // aligned columns, so the whole group's base product is one reduction-contiguous operand.
+    if (nt % 8) return -CT_EINVAL_SHAPE;
+    for (int i = 0; i < count; ++i) {
+        const void *wd = w_dense ? w_dense[i] : nullptr;
+        const ct_nf4_weight *wq = w_nf4 ? w_nf4[i] : nullptr;
+        if (!wd == !wq || n[i] % 8 || (r[i] > 0 && !b[i])) return -CT_EINVAL_POINTER;
+        if (wq) {
+            if (const int st = validate_nf4(wq)) return st;
+            if (wq->rows != n[i] || wq->cols != k) return -CT_EINVAL_SHAPE;
+            if (!nf4_transposable(wq)) return -CT_EINVAL_LAYOUT;
+        }
+    }
+    void *wbuf = nullptr;
+    if (const int st = take_weight(workspace, workspace_bytes, nt, k, wbuf)) return st;
+    int64_t col = 0;
+    for (int i = 0; i < count; ++i) {
+        uint16_t *dst = static_cast<uint16_t *>(wbuf) + col;
+        hipError_t e;
+        if (w_nf4 && w_nf4[i]) {
+            e = nf4_dequant_transposed(w_nf4[i], dst, stream, nt);
+        } else {
+            transpose_bf16<<<dim3((unsigned)cdiv(k, 64), (unsigned)cdiv(n[i], 64)), 256, 0, stream>>>(
+                static_cast<const uint16_t *>(w_dense[i]), k, n[i], k, dst, nt);
+            e = hipGetLastError();
+        }
+        if (e != hipSuccess) return to_status(e);
+        col += n[i];
+    }
+    // low_i = dy_i b_i into low's columns
+    col = 0;
+    int64_t rcol = 0;
+    for (int i = 0; i < count; ++i) {
+        if (r[i] > 0) {
+            const int slot = profile_open(CT_PROF_LOWRANK, stream);
+            const int st = ct_gemm(static_cast<const uint16_t *>(dy) + col, lddy, 0, b[i], r[i], 0,
+                                   static_cast<uint16_t *>(low) + rcol, ldlow, CT_BF16, nullptr, 0, m, r[i], n[i],
+                                   workspace, workspace_bytes, stream);
+            profile_close(slot, stream, 2.0 * m * r[i] * n[i]);
+            if (st) return st;
+        }
+        col += n[i];
+        rcol += r[i];
+    }
+    // dx (+)= [dy | low] [W^T ; a_stack]: one contraction over n_total + r_total columns
+    Problem pr{};
+    pr.p.seg[0].a = dense(dy, lddy);
+    pr.p.seg[0].b = dense(wbuf, nt);
+    pr.p.seg[0].k = nt;
+    pr.p.seg[1].a = dense(low, ldlow);
+    pr.p.seg[1].b = dense(a_stack, k);
+    pr.p.seg[1].k = rt;
+    pr.p.nseg = rt > 0 ? 2 : 1;
+    pr.p.m = m;
+    pr.p.n = k;
+    pr.p.c = dx;
+    pr.p.ldc = lddx;
+    pr.p.beta = add;
+    pr.src[0] = SRC_KC;
+    pr.src[1] = SRC_KC;
+    pr.src[2] = SRC_KC;
+    pr.src[3] = SRC_KS;
+    pr.out = CT_BF16;
+    pr.splits = 1;
+    pr.tile = -1;
+    pr.ws = workspace;
+    pr.ws_bytes = workspace ? workspace_bytes : 0;
+    pr.vec = vec_ok(pr);
+    const int slot = profile_open(CT_PROF_DX_GEMM, stream);
+    const hipError_t e = run(pr, stream);
+    profile_close(slot, stream, 2.0 * m * k * (double)(nt + rt));
     return to_status(e);
 }
 

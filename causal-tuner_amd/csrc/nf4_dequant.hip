@@ -205,7 +205,7 @@ template <bool NESTED, int STORAGE>
 __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_t(
     const uint8_t *__restrict__ packed, const void *__restrict__ absmax_ptr, const float *__restrict__ code,
     const float *__restrict__ code2, const float *__restrict__ absmax2, const float *__restrict__ offset_ptr,
-    uint16_t *__restrict__ out, int64_t rows, int64_t cols, int log2_block, int log2_block2) {
+    uint16_t *__restrict__ out, int64_t rows, int64_t cols, int log2_block, int log2_block2, int64_t ldo) {
     __shared__ float lds_code[16];
     __shared__ float lds_code2[NESTED ? 256 : 1];
     __shared__ uint32_t tile[128][32];
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_t(
         const int64_t oc = c0 + k, orow = r0 + 8 * chunk;
         const u32x4 val = *reinterpret_cast<const u32x4 *>(&tile[k][(4 * chunk) ^ (((k >> 4) & 3) << 3)]);
         if (oc < cols && orow < rows)
-            __builtin_nontemporal_store(val, reinterpret_cast<u32x4 *>(out + oc * rows + orow));
+            __builtin_nontemporal_store(val, reinterpret_cast<u32x4 *>(out + oc * ldo + orow));
     }
 }
 
@@ -330,23 +330,23 @@ double dequant_bytes(const ct_nf4_weight *w, int64_t n, int out_dtype) {
 }
 
 template <bool NESTED>
-hipError_t launch_transposed(const ct_nf4_weight *w, void *out, int lb, int lb2, hipStream_t stream) {
+hipError_t launch_transposed(const ct_nf4_weight *w, void *out, int64_t ldo, int lb, int lb2, hipStream_t stream) {
     const dim3 grid((unsigned)cdiv(w->rows, 64), (unsigned)cdiv(w->cols, 128));
     switch (w->storage_dtype) {
         case CT_BF16:
             nf4_dequant_t<NESTED, CT_BF16><<<grid, dim3(kDequantThreads), 0, stream>>>(
                 w->packed, w->absmax, w->code, w->code2, w->absmax2, w->offset, static_cast<uint16_t *>(out),
-                w->rows, w->cols, lb, lb2);
+                w->rows, w->cols, lb, lb2, ldo);
             break;
         case CT_F16:
             nf4_dequant_t<NESTED, CT_F16><<<grid, dim3(kDequantThreads), 0, stream>>>(
                 w->packed, w->absmax, w->code, w->code2, w->absmax2, w->offset, static_cast<uint16_t *>(out),
-                w->rows, w->cols, lb, lb2);
+                w->rows, w->cols, lb, lb2, ldo);
             break;
         default:
             nf4_dequant_t<NESTED, CT_F32><<<grid, dim3(kDequantThreads), 0, stream>>>(
                 w->packed, w->absmax, w->code, w->code2, w->absmax2, w->offset, static_cast<uint16_t *>(out),
-                w->rows, w->cols, lb, lb2);
+                w->rows, w->cols, lb, lb2, ldo);
     }
     return hipGetLastError();
 }
@@ -359,14 +359,17 @@ bool nf4_transposable(const ct_nf4_weight *w) {
            reinterpret_cast<uintptr_t>(w->packed) % 8 == 0 && cdiv(w->cols, 128) <= 65535;
 }
 
-// bf16 out[cols][rows] = the transpose of the decoded weight (same values as
-// ct_nf4_dequant with CT_BF16 output); out 16-byte aligned. Timed with the decoder family.
-hipError_t nf4_dequant_transposed(const ct_nf4_weight *w, void *out, hipStream_t stream) {
+// bf16 out[cols][ldo] = the transpose of the decoded weight (same values as
+// ct_nf4_dequant with CT_BF16 output) in the first `rows` elements of each output row;
+// out 16-byte aligned, ldo >= rows and a multiple of 8. Timed with the decoder family.
+hipError_t nf4_dequant_transposed(const ct_nf4_weight *w, void *out, hipStream_t stream, int64_t ldo) {
+    if (ldo <= 0) ldo = w->rows;
+    if (ldo < w->rows || ldo % 8 || reinterpret_cast<uintptr_t>(out) % 16) return hipErrorInvalidValue;
     const int lb = log2_exact(w->blocksize);
     const int lb2 = w->nested ? log2_exact(w->blocksize2) : 0;
     const int slot = profile_open(CT_PROF_DEQUANT, stream);
-    const hipError_t e = w->nested ? launch_transposed<true>(w, out, lb, lb2, stream)
-                                   : launch_transposed<false>(w, out, lb, lb2, stream);
+    const hipError_t e = w->nested ? launch_transposed<true>(w, out, ldo, lb, lb2, stream)
+                                   : launch_transposed<false>(w, out, ldo, lb, lb2, stream);
     profile_close(slot, stream, dequant_bytes(w, w->rows * w->cols, CT_BF16));
     return e;
 }

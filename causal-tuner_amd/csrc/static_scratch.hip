@@ -1,14 +1,14 @@
 // ct_forward_linear_static: ct_forward_linear for callers that cannot allocate device
-// memory (code under HIP graph capture, tight serving loops, harnesses that forbid
-// hipMalloc). Its scratch space -- the split partials of few-row problems and, from 512 rows
+// memory (tight serving loops, harnesses that forbid hipMalloc). Its scratch space -- the split partials of few-row problems and, from 512 rows
 // on, the decoded bf16 weight -- lives in one file-scope device array of
 // CT_STATIC_SCRATCH_BYTES per GPU instead of a caller's workspace. The array is created
 // when the library's code object loads on a device and held until the process ends.
 //
 // Host code never passes the array's name to a kernel: on the host that name is only a
 // stand-in. The device address is looked up once per device with hipGetSymbolAddress
-// (with that device current) and kept; every later call on that device uses the kept
-// address. All calls on one GPU share its array, so calls that overlap on one GPU (two
+// (with that device current) by ct_init_device, the library's set-up call, and kept;
+// every later call on that device uses the kept address (a first static call on a device
+// that was never set up looks it up itself). All calls on one GPU share its array, so calls that overlap on one GPU (two
 // streams, two threads) race on it; the array keeps the last call's contents, and every
 // kernel that reads it first writes what it reads (split partials are fully written
 // before the reduction, the decoded weight before the GEMM).
@@ -27,7 +27,7 @@ constexpr int kMaxDevices = 64;
 std::mutex g_lookup;
 std::atomic<void *> g_address[kMaxDevices];
 
-// Device address of the current device's scratch array (looked up on the first call there).
+// Device address of the current device's scratch array (looked up once per device).
 int scratch_address(void **out) {
     int device = -1;
     hipError_t e = hipGetDevice(&device);
@@ -49,6 +49,11 @@ int scratch_address(void **out) {
 }
 
 }  // namespace
+
+extern "C" int ct_init_device(void) {
+    void *p = nullptr;
+    return scratch_address(&p);
+}
 
 extern "C" int ct_forward_linear_static(const void *x, int64_t ldx, const void *w_dense, const ct_nf4_weight *w_nf4,
                                         const void *a, const void *b, const void *bias, void *out, int64_t ldo,

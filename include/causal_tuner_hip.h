@@ -85,6 +85,14 @@ typedef struct ct_nf4_weight {
 } ct_nf4_weight;
 
 int ct_abi_version(void);
+
+/*
+ * Per-device set-up, once per GPU with that GPU current (idempotent, thread-safe):
+ * resolves the device address of the static scratch array that ct_forward_linear_static
+ * uses on this GPU, so that no later call runs a runtime symbol query. No counterpart in
+ * the reference (its Triton kernels need no set-up). Returns 0 or a hipError_t.
+ */
+int ct_init_device(void);
 const char *ct_status_string(int status);
 
 /*
@@ -319,18 +327,19 @@ int ct_forward_linear(const void *x, int64_t ldx,
 
 /*
  * ct_forward_linear without a workspace argument, for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). No counterpart in the reference, whose operators allocate their workspaces
- * with torch (kernels/linear.py:67,74). Same arguments, results and row regimes as
- * ct_forward_linear, which it calls with the library's static device scratch array of
- * CT_STATIC_SCRATCH_BYTES per GPU (held from the library's load on that GPU until the process
- * ends) in place of the workspace. A problem whose ct_forward_linear_workspace exceeds
+ * memory (tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference, whose operators allocate their workspaces with torch (kernels/linear.py:67,74).
+ * Same arguments, results and row regimes as ct_forward_linear, which it calls with the
+ * library's static device scratch array of CT_STATIC_SCRATCH_BYTES per GPU (held from the
+ * library's load on that GPU until the process ends) in place of the workspace. Its device
+ * address is resolved once per GPU by ct_init_device (or, on a GPU never set up, by the
+ * first static call there). A problem whose ct_forward_linear_workspace exceeds
  * CT_STATIC_SCRATCH_BYTES returns -CT_EINVAL_WORKSPACE before anything is enqueued: 64 MiB
  * covers every few-row problem and the many-row ones whose decoded weight, plus the
  * split partials where the reduction is split, fits (up to about 32 M weight elements
  * without a split). It calls no allocator. Every call on one GPU uses that GPU's
  * one array: calls that overlap on a GPU (two streams or threads) race and must be ordered
- * by the caller.
+ * by the caller. Capture of these calls into a HIP graph is not supported.
  */
 #define CT_STATIC_SCRATCH_BYTES (64LL << 20)
 int ct_forward_linear_static(const void *x, int64_t ldx,
@@ -339,6 +348,27 @@ int ct_forward_linear_static(const void *x, int64_t ldx,
                              void *out, int64_t ldo, void *xa, int64_t ldxa, int32_t xa_given,
                              int64_t m, int64_t n, int64_t k, int64_t r,
                              const ct_epilogue *epilogue, hipStream_t stream);
+
+/*
+ * Replaces the forward of two projections that read one input with one rank, when their
+ * xa are given (the stacked x [a_1; a_2]^T of ct_gemm): forward_linear per projection in
+ * _LoRAGroup.forward (kernels/linear.py:72-86) for gate and up. For i < 2:
+ *   out_i = bf16(x w_i^T + xa[:, i r : (i + 1) r] b_i^T)        [m, n_i] (ldo[i])
+ * as one GEMM over [w_1; w_2] (n_1 + n_2 output columns), so the two share one grid of
+ * tiles: one partial last round of 256 x 256 tiles instead of two. The results are those
+ * of ct_forward_linear with xa_given per projection (the same products and sums). x [m, k]
+ * (ldx, k % 8 == 0), w_dense[i] bf16 [n_i, k] or w_nf4[i] (exactly one per projection),
+ * b_stack bf16 [n_1 + n_2, r] = [b_1; b_2] (contiguous), xa [m, 2 r] (ldxa). n_1 is a
+ * multiple of 256; no bias, no elementwise step. Needs m > 64 (-CT_EINVAL_SHAPE
+ * otherwise: the caller runs the projections one by one); the reduction is never split.
+ * The weights are decoded (or copied) side by side into the workspace first, whose size
+ * ct_group_forward_workspace gives (count must be 2).
+ */
+int64_t ct_group_forward_workspace(int64_t m, int32_t count, const int64_t *n, int64_t k, int64_t r);
+int ct_group_forward(const void *x, int64_t ldx, int32_t count, const int64_t *n,
+                     const void *const *w_dense, const ct_nf4_weight *const *w_nf4, const void *b_stack,
+                     const void *xa, int64_t ldxa, void *const *out, const int64_t *ldo, int64_t m, int64_t k,
+                     int64_t r, void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * Replaces input_gradient (kernels/linear.py:36-39):
@@ -360,6 +390,33 @@ int ct_input_gradient(const void *dy, int64_t lddy,
                       int64_t m, int64_t n, int64_t k, int64_t r, int32_t add,
                       const ct_epilogue *epilogue,
                       void *workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Replaces the dx half of the grouped backward of projections that share an input:
+ * _LoRAGroup.backward's input_gradient per projection with add = index > 0
+ * (kernels/linear.py:107-122, q/k/v) and the tiled MLP's gate and up
+ * (kernels/mlp_cuda.py:136-140). For i < count (count <= CT_GROUP_MAX):
+ *   low_i = bf16(dy_i b_i)                                    [m, r_i] (columns of low)
+ *   dx    = bf16(sum_i (dy_i w_i + low_i a_i) (+ dx if add))  [m, k]
+ * The sum is one contraction over n_total + r_total reduction columns with fp32
+ * accumulation and one rounding; the reference rounds dx to bf16 after each projection,
+ * so this is within its tolerances and closer to the float64 oracle. dy [m, n_total] holds
+ * dy_1 .. dy_count side by side (lddy); w_i is w_dense[i] (bf16 [n_i, k]) or w_nf4[i]
+ * (rows n_i, cols k, decodable transposed: cols % 16 == 0, rows % 8 == 0), exactly one per
+ * projection (either array may be null when the other holds every weight); a_stack bf16
+ * [r_total, k] = [a_1; ...; a_count] (contiguous rows); b[i] bf16 [n_i, r_i] contiguous;
+ * low bf16 [m, r_total] (ldlow). Every n_i is a multiple of 8. The weights are decoded
+ * (or, dense, transposed) side by side into the workspace first, whose size
+ * ct_group_input_gradient_workspace gives; the low-rank products and the contraction's
+ * split partials use the rest.
+ */
+#define CT_GROUP_MAX 8
+int64_t ct_group_input_gradient_workspace(int64_t m, int32_t count, const int64_t *n, const int64_t *r, int64_t k);
+int ct_group_input_gradient(const void *dy, int64_t lddy, int32_t count, const int64_t *n, const int64_t *r,
+                            const void *const *w_dense, const ct_nf4_weight *const *w_nf4,
+                            const void *a_stack, const void *const *b,
+                            void *dx, int64_t lddx, void *low, int64_t ldlow, int64_t m, int64_t k, int32_t add,
+                            void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * Replaces parameter_gradients (kernels/linear.py:42-44) with accumulate's fp32 branch
@@ -408,7 +465,10 @@ int ct_silu_multiply(const void *gate, const void *up, void *h, void *dgate, voi
 /*
  * Replaces the partial GPT-J rotary kernels `_rope` and `_owned_qk_rope` with
  * `_rotate_pair` (kernels/core_cuda.py:133-189). x and y are [tokens, heads, head_dim]
- * contiguous of `dtype` (CT_F32, CT_F16 or CT_BF16); cosine and sine are [tokens, half]
+ * of `dtype` (CT_F32, CT_F16 or CT_BF16), contiguous within a token, with ldx / ldy
+ * elements between tokens (0: heads * head_dim, contiguous; a larger pitch lets y be a
+ * column range of a wider matrix, as the grouped backward's side-by-side upstream
+ * gradients); x == y needs ldx == ldy. cosine and sine are [tokens, half]
  * contiguous of `trig_dtype`, half <= head_dim / 2. Channel pairs (2c, 2c+1), c < half:
  *   e' = T(T(e cos) - T(o sin)),  o' = T(T(o cos) + T(e sin))    (T = round to dtype)
  * with the sine negated when `inverse` (the backward rotation). With rotated_only = 0
@@ -417,8 +477,8 @@ int ct_silu_multiply(const void *gate, const void *up, void *h, void *dgate, voi
  * rotate_owned_qk does on freshly written projection outputs.
  */
 int ct_rope(const void *x, void *y, const void *cosine, const void *sine, int64_t tokens, int64_t heads,
-            int64_t head_dim, int64_t half, int32_t inverse, int32_t rotated_only, int32_t dtype,
-            int32_t trig_dtype, hipStream_t stream);
+            int64_t head_dim, int64_t half, int64_t ldx, int64_t ldy, int32_t inverse, int32_t rotated_only,
+            int32_t dtype, int32_t trig_dtype, hipStream_t stream);
 
 /*
  * Kernel timing for benchmarks; no counterpart in the reference (which publishes no kernel

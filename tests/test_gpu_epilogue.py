@@ -137,6 +137,19 @@ def test_epilogue_rejected_with_accumulation_and_bad_shapes():
         _forward(x, base.matrix, None, a, b, None, out, xa, False, missing)
 
 
+def test_epilogue_rejects_strided_or_mixed_rotary_tables():
+    """The fused rotation reads [rows, half] tables with a row pitch of half and one dtype:
+    column slices of a wider table, tables of two dtypes or of another row count are
+    refused on the host (the separate ct_rope pass validates its own)."""
+    from causal_tuner.kernels import _native
+    wide = torch.ones(32, 4, device="cuda")
+    for cosine, sine in ((wide[:, :2], wide[:, 2:]),
+                         (torch.ones(32, 2, device="cuda"), torch.ones(32, 2, device="cuda", dtype=torch.bfloat16)),
+                         (torch.ones(31, 2, device="cuda"), torch.ones(31, 2, device="cuda"))):
+        with pytest.raises(ValueError, match="rotary tables"):
+            _native.epilogue(_native.CT_EPI_ROPE, 32, rotary=(cosine, sine, 8))
+
+
 def _unfused(monkeypatch):
     from causal_tuner.kernels import linear, mlp_cuda
     monkeypatch.setattr(linear, "fusable", lambda *tensors: False)

@@ -41,6 +41,31 @@ def test_fused_loss_large_vocabulary_and_scaled_gradient(vocab, dtype):
     torch.testing.assert_close(head.grad, expected_head, rtol=.01, atol=1e-4)
 
 
+@pytest.mark.parametrize("vocab", [97, 4099])
+def test_fused_loss_float16_compute_with_float32_head(vocab):
+    """A float16 compute dtype with a float32 trainable head: the head gradient accumulates
+    d^T x with fp16 operands into fp32, which the reference does with addmm on operands cast
+    to the output dtype (kernels/linear.py:22-23, called from loss_cuda.py:145)."""
+    from causal_tuner.kernels.loss import projection_loss
+    dtype = torch.float16
+    x = torch.randn(1, 7, 32, device="cuda", dtype=dtype, requires_grad=True)
+    head = (torch.randn(vocab, 32, device="cuda", dtype=torch.float32) * .1).requires_grad_()
+    labels = torch.randint(vocab, (1, 7), device="cuda")
+    weights = torch.tensor([[0, .1, 1, .5, 0, 2, .2]], device="cuda")
+    actual = projection_loss(x, head, labels, weights, token_budget=3, compute_dtype=dtype)
+    expected, logits = _full(x, head, labels, weights, dtype)
+    torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-3)
+    actual.backward()
+    derivative = logits.softmax(-1)
+    derivative[torch.arange(7, device="cuda"), labels.flatten()] -= 1
+    derivative = (derivative * weights.flatten()[:, None]).to(dtype)
+    expected_head = derivative.float().T @ x.detach().flatten(0, 1).float()
+    assert head.grad.dtype == torch.float32
+    torch.testing.assert_close(head.grad, expected_head, rtol=.01, atol=1e-4)
+    expected_x = (derivative.float() @ head.detach().to(dtype).float()).to(dtype).view_as(x)
+    torch.testing.assert_close(x.grad, expected_x, rtol=.01, atol=1e-3)
+
+
 @pytest.mark.parametrize("supervised", [False, True])
 def test_fused_loss_cached_gradients_can_be_reused(supervised):
     from causal_tuner.kernels.loss import projection_loss

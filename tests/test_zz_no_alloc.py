@@ -36,6 +36,7 @@ def _run(entry, problem, m, k, n, r):
               out.data_ptr(), n, xa.data_ptr(), r, 0, m, n, k, r)
     stream = _native.stream_of(x)
     if entry == "static":
+        assert lib.ct_init_device() == 0   # the library's per-device set-up, before any static call
         status = lib.ct_forward_linear_static(*common, None, stream)
     else:
         need = lib.ct_forward_linear_workspace(m, n, k, r, 1)
