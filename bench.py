@@ -189,7 +189,11 @@ def projection_measure(device, shapes, rows_list, iters=20, rank=R):
     (HIP events; the rates use it), the GPU's own time per step (the steps queued behind
     a spin kernel, so host-side work is hidden), algorithmic TFLOP/s and GB/s, and the
     fraction of the bound that applies (HBM for few rows, bf16 MFMA for many). Under the
-    C3 step's projection budget, as there."""
+    C3 step's projection budget, as there.
+    `ms` runs the backward on the calling thread (torch.autograd.set_multithreading_enabled
+    (False)); `ms_engine_thread` is the same step with autograd's default per-device worker
+    thread, whose hand-off from the calling thread costs ~0.1 ms per backward on MI355X
+    boxes (measured) -- the dominant host cost of a few-row step, outside this library."""
     from causal_tuner.kernels.linear import project_group, projection_budget
     from causal_tuner.modeling.lora import Projection
     results = {}
@@ -207,7 +211,9 @@ def projection_measure(device, shapes, rows_list, iters=20, rank=R):
                 with projection_budget(PROJECTION_BUDGET):
                     out, = project_group((module,), x)
                 torch.autograd.grad(out, (x, module.lora_A, module.lora_B), dy)
-            ms = time_events(step, iters)
+            with torch.autograd.set_multithreading_enabled(False):
+                ms = time_events(step, iters)
+            ms_engine = time_events(step, iters)
             # the same steps queued behind a spin kernel: the GPU's own time per step, which
             # the host-side operator path (autograd, ctypes calls) hides at few rows
             gpu_ms = _events_us(step, iters) * 1e-3
@@ -215,14 +221,21 @@ def projection_measure(device, shapes, rows_list, iters=20, rank=R):
             tflops, gbs = flops / (ms * 1e-3) / 1e12, nbytes / (ms * 1e-3) / 1e9
             bound = "hbm" if flops / nbytes < BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma"
             frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tflops / BF16_PEAK_TFLOPS
-            results[f"{k}->{n} M{m}"] = {"ms": round(ms, 4), "gpu_ms": round(gpu_ms, 4), "TFLOP/s": round(tflops, 2),
+            results[f"{k}->{n} M{m}"] = {"ms": round(ms, 4), "ms_engine_thread": round(ms_engine, 4),
+                                         "gpu_ms": round(gpu_ms, 4), "TFLOP/s": round(tflops, 2),
                                          "GB/s": round(gbs, 1), "bound": bound, "frac": round(frac, 4)}
-            log(f"  {k}->{n} M={m:6d}: {ms:8.3f} ms (GPU {gpu_ms:.3f} ms)  {tflops:8.2f} TFLOP/s  "
+            log(f"  {k}->{n} M={m:6d}: {ms:8.3f} ms (engine thread {ms_engine:.3f}, GPU {gpu_ms:.3f} ms)  "
+                f"{tflops:8.2f} TFLOP/s  "
                 f"{gbs:8.1f} GB/s  {bound} {100 * frac:.1f}%")
             del x, dy
         del module
         torch.cuda.empty_cache()
     return results
+
+
+def projection_sweep(device):
+    return {"C1": projection_measure(device, [(1024, 1024)], [512], rank=16),
+            "C5": projection_measure(device, [(6144, 24576), (24576, 6144)], [16, 64, 256, 16384], iters=10)}
 
 
 def _timed(fn, budget_s, max_reps=50):
@@ -537,7 +550,13 @@ def epilogue_measure(device, rows=4096, reps=20, rank=R):
         def both():
             plain()
             separate()
-        t_plain, t_fused, t_both = (_events_us(fn, reps) for fn in (plain, fused, both))
+        # five interleaved rounds, the fastest of each: sides that run the same kernels (the
+        # SiLU steps on 256 x 256 tiles take the separate pass) then differ by noise only
+        times = {"plain": [], "fused": [], "both": []}
+        for _ in range(5):
+            for key, fn in (("plain", plain), ("fused", fused), ("both", both)):
+                times[key].append(_events_us(fn, reps))
+        t_plain, t_fused, t_both = (min(times[key]) for key in ("plain", "fused", "both"))
         results[name] = {"rows": m, "in": k, "out": n, "call_us": round(t_plain, 1),
                          "with_step_us": round(t_fused, 1), "call_then_separate_us": round(t_both, 1),
                          "saved_us": round(t_both - t_fused, 1)}
@@ -635,6 +654,8 @@ def main():
                         help="run only the C5 few-row kernel leg and print its JSON")
     parser.add_argument("--epilogue-only", action="store_true",
                         help="run only the projection-epilogue leg (C4 shapes) and print its JSON")
+    parser.add_argument("--projections-only", action="store_true",
+                        help="run only the C1/C5 projection legs and print their JSON")
     parser.add_argument("--no-c4", action="store_true", help="skip the C4 training-step leg")
     parser.add_argument("--c4-only", action="store_true", help="run only the C4 training-step leg")
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MiB",
@@ -660,6 +681,9 @@ def main():
         return
     if args.c4_only:
         print(json.dumps({"c4": c4_measure(device)}), flush=True)
+        return
+    if args.projections_only:
+        print(json.dumps({"projections": projection_sweep(device)}), flush=True)
         return
     if args.epilogue_only:
         print(json.dumps({"epilogues": epilogue_measure(device)}), flush=True)
@@ -730,8 +754,7 @@ def main():
     sweep = None
     if not args.no_sweep:
         log("C1 and C5 projections (fwd+bwd, NF4 base, one projection):")
-        sweep = {"C1": projection_measure(device, [(1024, 1024)], [512], rank=16),
-                 "C5": projection_measure(device, [(6144, 24576), (24576, 6144)], [16, 64, 256, 16384], iters=10)}
+        sweep = projection_sweep(device)
     skinny = None
     if not args.no_sweep:
         log("C5 few-row kernels (M 16 and 64, weights rotated past the Infinity Cache):")
@@ -767,7 +790,9 @@ def main():
         "dequant": {"workload": "C2: standalone NF4 dequant to bf16", "bound": "hbm", "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "results": dequant},
         "projections": {"workload": "C1 (M 512, 1024->1024, rank 16) and C5 (6144<->24576, M 16..16384, rank "
-                                    "256): one NF4-LoRA projection fwd+bwd through project_group + autograd",
+                                    "256): one NF4-LoRA projection fwd+bwd through project_group + autograd; "
+                                    "ms with the backward on the calling thread, ms_engine_thread with "
+                                    "autograd's per-device worker thread",
                         "results": sweep},
         "skinny": {"workload": "C5 M 16 and 64: the forward and dx GEMM kernels alone on the packed NF4 weight "
                                "(split reduction included), four weight copies in rotation",

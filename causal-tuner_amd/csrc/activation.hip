@@ -125,6 +125,20 @@ hipError_t silu_forward_flat(const uint16_t *gate, const uint16_t *up, uint16_t 
     return hipGetLastError();
 }
 
+// The backward twin: reads gate, up and the upstream gradient in h, writes dgate, dup and
+// the reconstructed h over it (ct_silu_multiply's backward kernel and bits). The outputs
+// may alias gate and up (each lane reads its chunk before writing it).
+hipError_t silu_backward_flat(const uint16_t *gate, const uint16_t *up, uint16_t *h, uint16_t *dg, uint16_t *du,
+                              int64_t n, hipStream_t s) {
+    if (n % 8 || !aligned16(gate) || !aligned16(up) || !aligned16(h) || !aligned16(dg) || !aligned16(du))
+        return hipErrorInvalidValue;
+    const int64_t chunks = n / 8;
+    silu_multiply_vec<true, true><<<dim3((unsigned)cdiv(chunks, 256)), dim3(256), 0, s>>>(
+        reinterpret_cast<const uint4 *>(gate), reinterpret_cast<const uint4 *>(up), reinterpret_cast<uint4 *>(h),
+        reinterpret_cast<uint4 *>(dg), reinterpret_cast<uint4 *>(du), chunks);
+    return hipGetLastError();
+}
+
 }  // namespace ct
 
 extern "C" int ct_silu_multiply(const void *gate, const void *up, void *h, void *dgate, void *dup, int64_t n,
