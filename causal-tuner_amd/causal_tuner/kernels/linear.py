@@ -92,10 +92,19 @@ def _query(name, *args):
     return getattr(_native.library(), name)(*args)
 
 
+_NO_WORKSPACE = {}
+
+
 def _workspace(nbytes, device):
     """Caller-owned scratch for split reductions (the kernels never allocate); torch's
-    caching allocator makes the per-call allocation cheap."""
-    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+    caching allocator makes the per-call allocation cheap. A call that needs none gets one
+    empty tensor per device (a null pointer and 0 bytes), with no allocation."""
+    if nbytes <= 0:
+        empty = _NO_WORKSPACE.get(device)
+        if empty is None:
+            empty = _NO_WORKSPACE[device] = torch.empty(0, dtype=torch.uint8, device=device)
+        return empty
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
 
 
 class _Output:
@@ -232,7 +241,7 @@ def group_factors(parameters, count, dtype, x, shared=None):
     Returns (factors, stacked or None) with factors = [a_1, b_1, a_2, b_2, ...]."""
     shared = count if shared is None else shared
     tensors = [value for i in range(count) for value in parameters[i*4+1:i*4+3]]
-    ranks = {len(tensors[2*i]) for i in range(shared)}
+    ranks = {tensors[2*i].shape[0] for i in range(shared)}
     if (shared > 1 and x.is_cuda and dtype == torch.bfloat16 and len(ranks) == 1 and ranks != {0}
             and len({tensors[2*i].shape[1] for i in range(shared)}) == 1):
         r = ranks.pop()
@@ -444,7 +453,7 @@ def stacked_rows(tensors):
         if not t.is_contiguous() or t.shape[1] != width or t.data_ptr() != offset:
             return torch.cat(tensors)
         offset += t.numel() * t.element_size()
-    return first.as_strided((sum(len(t) for t in tensors), width), (width, 1))
+    return first.as_strided((sum(t.shape[0] for t in tensors), width), (width, 1))
 
 
 def group_input_gradient(bases, dy, widths, ranks, a_stack, bs, dx, low, add):
@@ -547,7 +556,7 @@ class _Base:
                 self.state = state
         if self.state is None:
             self.matrix = materialize(weight, state, dtype)
-        self.rows = int(state.shape[0]) if state is not None else len(weight)
+        self.rows = int(state.shape[0]) if state is not None else weight.shape[0]
 
     def forward(self, x, a, b, bias, out, xa, xa_given=False, epilogue=None):
         """out = x w^T + (x a^T) b^T (+ bias). Device only: with xa_given, xa holds x a^T
@@ -599,8 +608,8 @@ def group_row_bytes(parameters, count, element, head_dim):
     """Device bytes per input row that one whole-input tile of a group holds across its
     forward and backward: every kept xa, the backward's [rows, r] gradient product and,
     with rotary outputs, the inverse-rotation scratch of a q or k gradient."""
-    ranks = [len(parameters[4*i+1]) for i in range(count)]
-    widths = [len(parameters[4*i+2]) for i in range(min(count, 2))] if head_dim else [0]
+    ranks = [parameters[4*i+1].shape[0] for i in range(count)]
+    widths = [parameters[4*i+2].shape[0] for i in range(min(count, 2))] if head_dim else [0]
     return element * (sum(ranks) + max(ranks, default=0) + max(widths, default=0))
 
 
@@ -630,19 +639,20 @@ class _LoRAGroup(torch.autograd.Function):
     def forward(ctx, x, dtype, tile, states, cosine, sine, head_dim, residual, *parameters):
         count = len(states)
         flat = x.reshape(-1, x.shape[-1]).to(dtype)
+        total = flat.shape[0]
         element = dtype.itemsize
-        step, keep = _plan_rows(len(flat), tile, _KEEP_BUDGET.get(),
+        step, keep = _plan_rows(total, tile, _KEEP_BUDGET.get(),
                                 group_row_bytes(parameters, count, element, head_dim))
         ctx.dtype, ctx.states, ctx.head_dim, ctx.step = dtype, states, head_dim, step
         factors, stack = group_factors(parameters, count, dtype, x)
         bases = [_Base(parameters[4*i], state, dtype) for i, state in enumerate(states)]
         biases = [None if parameters[4*i+3] is None else parameters[4*i+3].to(dtype) for i in range(count)]
-        outputs = [torch.empty((len(flat), base.rows), device=x.device, dtype=dtype) for base in bases]
-        ranks = [len(parameters[4*i+1]) for i in range(count)]
-        span = min(step, len(flat))
+        outputs = [torch.empty((total, base.rows), device=x.device, dtype=dtype) for base in bases]
+        ranks = [parameters[4*i+1].shape[0] for i in range(count)]
+        span = min(step, total)
         # xa of every projection for the rows of one tile (all rows when kept), as column
         # slices of one buffer so a stacked GEMM fills them together.
-        xa = torch.empty((len(flat) if keep else span, sum(ranks)), device=x.device, dtype=dtype)
+        xa = torch.empty((total if keep else span, sum(ranks)), device=x.device, dtype=dtype)
         columns = [xa[:, sum(ranks[:i]):sum(ranks[:i+1])] for i in range(count)]
         # The rotation of q/k (core_cuda.py:192-200) and the residual add (linear.py:90-91)
         # run in the GEMM epilogue when the operands allow it, else as separate passes.
@@ -650,14 +660,14 @@ class _LoRAGroup(torch.autograd.Function):
         trig = None
         if rotated:
             half = cosine.shape[-1]
-            trig = tuple(value.reshape(-1, half) if value.numel() == len(flat) * half else None
+            trig = tuple(value.reshape(-1, half) if value.numel() == total * half else None
                          for value in (cosine, sine))
         # the fused step reads [rows, half] tables with a row pitch of half and one dtype;
         # anything else takes the separate pass, which validates the tables itself
         rope_fused = bool(rotated) and trig[0] is not None and trig[1] is not None and \
             trig[0].is_contiguous() and trig[1].is_contiguous() and trig[0].dtype == trig[1].dtype and \
             fusable(*outputs[:rotated]) and all(out.shape[1] % head_dim == 0 for out in outputs[:rotated])
-        residual_flat = None if residual is None else residual.reshape(len(flat), -1)
+        residual_flat = None if residual is None else residual.reshape(total, -1)
         residual_fused = residual_flat is not None and not rotated and fusable(outputs[0], residual_flat)
         # Two projections of one rank without biases or steps (gate and up) share one grid of
         # output tiles from GROUP_FORWARD_ROWS rows: one partial last round instead of two.
@@ -666,22 +676,23 @@ class _LoRAGroup(torch.autograd.Function):
                                           biases))
         if paired:
             b_stack = stacked_rows([factors[1], factors[3]])
-        for start in range(0, len(flat), step):
+        for start in range(0, total, step):
             part = flat[start:start+step]
-            rows = slice(start, start+len(part)) if keep else slice(0, len(part))
-            window = slice(start, start+len(part))
+            n_part = part.shape[0]
+            rows = slice(start, start+n_part) if keep else slice(0, n_part)
+            window = slice(start, start+n_part)
             if stack is not None:
                 _low_rank(part, stack, xa[rows], transpose=True)
-            if paired and len(part) > 64:
+            if paired and n_part > 64:
                 group_forward(bases, part, b_stack, xa[rows], [out[window] for out in outputs])
                 continue
             for index, base in enumerate(bases):
                 epilogue = None
                 if rope_fused and index < rotated:
-                    epilogue = _native.epilogue(_native.CT_EPI_ROPE, len(part),
+                    epilogue = _native.epilogue(_native.CT_EPI_ROPE, n_part,
                                                 rotary=(trig[0][window], trig[1][window], head_dim))
                 elif residual_fused and index == 0:
-                    epilogue = _native.epilogue(_native.CT_EPI_RESIDUAL, len(part), in0=residual_flat[window])
+                    epilogue = _native.epilogue(_native.CT_EPI_RESIDUAL, n_part, in0=residual_flat[window])
                 base.forward(part, factors[2*index], factors[2*index+1], biases[index], outputs[index][window],
                              columns[index][rows], xa_given=stack is not None, epilogue=epilogue)
         # Under a projection budget the backward also reuses the compute-dtype factors
@@ -705,19 +716,20 @@ class _LoRAGroup(torch.autograd.Function):
         parameters, kept = rest[:4*count], rest[4*count:4*count+count]
         saved_factors = rest[4*count+count:]
         flat = x.reshape(-1, x.shape[-1]).to(ctx.dtype)
+        total = flat.shape[0]
         dx = torch.empty_like(flat) if ctx.needs_input_grad[0] else None
         if ctx.head_dim:
             cosine, sine = (value.reshape(-1, value.shape[-1]) for value in (cosine, sine))
-        step, span = ctx.step, min(ctx.step, len(flat))
+        step, span = ctx.step, min(ctx.step, total)
         if saved_factors:
             factors, stack = list(saved_factors), None
         else:
             factors, stack = group_factors(parameters, count, ctx.dtype, x)
         bases = [_Base(parameters[4*i], state, ctx.dtype) if dx is not None else None
                  for i, state in enumerate(ctx.states)]
-        ranks = [len(parameters[4*i+1]) for i in range(count)]
+        ranks = [parameters[4*i+1].shape[0] for i in range(count)]
         signals = [grad.reshape(-1, grad.shape[-1]).to(ctx.dtype) for grad in grad_outputs]
-        allocate = torch.empty_like if len(flat) else torch.zeros_like
+        allocate = torch.empty_like if total else torch.zeros_like
         gradients = [(allocate(parameters[4*i+1]), allocate(parameters[4*i+2])) for i in range(count)]
         xa = None if kept else torch.empty((span, sum(ranks)), device=x.device, dtype=ctx.dtype)
         rotated = min(count, 2) if ctx.head_dim else 0
@@ -743,52 +755,53 @@ class _LoRAGroup(torch.autograd.Function):
             low = torch.empty((span, max(ranks)), device=x.device, dtype=ctx.dtype)
         scratch = (torch.empty(span * max(signals[i].shape[1] for i in range(rotated)), device=x.device,
                                dtype=ctx.dtype) if rotated and not grouped else None)
-        for start in range(0, len(flat), step):
+        for start in range(0, total, step):
             part = flat[start:start+step]
+            n_part = part.shape[0]
             if not kept:
                 if stack is not None:
-                    _low_rank(part, stack, xa[:len(part)], transpose=True)
+                    _low_rank(part, stack, xa[:n_part], transpose=True)
                 else:
                     for index in range(count):
                         columns_xa = slice(sum(ranks[:index]), sum(ranks[:index+1]))
-                        _low_rank(part, factors[2*index], xa[:len(part), columns_xa], transpose=True)
+                        _low_rank(part, factors[2*index], xa[:n_part, columns_xa], transpose=True)
             if grouped:
                 tile_signals = []
                 for index in range(count):
-                    signal = signals[index][start:start+len(part)]
-                    target = joined[:len(part), columns[index]]
+                    signal = signals[index][start:start+n_part]
+                    target = joined[:n_part, columns[index]]
                     if index < rotated:
                         from .core_cuda import inverse_rope_tile
-                        signal = inverse_rope_tile(signal, cosine[start:start+len(part)],
-                                                   sine[start:start+len(part)], ctx.head_dim, target)
+                        signal = inverse_rope_tile(signal, cosine[start:start+n_part],
+                                                   sine[start:start+n_part], ctx.head_dim, target)
                     else:
                         target.copy_(signal)
                         signal = target
                     tile_signals.append(signal)
-                group_input_gradient(bases, joined[:len(part)], widths, ranks, a_stack,
-                                     [factors[2*i+1] for i in range(count)], dx[start:start+len(part)],
-                                     low[:len(part)], False)
+                group_input_gradient(bases, joined[:n_part], widths, ranks, a_stack,
+                                     [factors[2*i+1] for i in range(count)], dx[start:start+n_part],
+                                     low[:n_part], False)
                 for index in range(count):
-                    inputs = (kept[index][start:start+len(part)] if kept else
-                              xa[:len(part), sum(ranks[:index]):sum(ranks[:index+1])])
+                    inputs = (kept[index][start:start+n_part] if kept else
+                              xa[:n_part, sum(ranks[:index]):sum(ranks[:index+1])])
                     parameter_gradients(part, tile_signals[index], *gradients[index],
-                                        low[:len(part), low_columns[index]], inputs, add=start > 0)
+                                        low[:n_part, low_columns[index]], inputs, add=start > 0)
                 continue
             for index in range(count):
                 a, b = factors[2*index], factors[2*index+1]
-                signal = signals[index][start:start+len(part)]
+                signal = signals[index][start:start+n_part]
                 if index < rotated:
                     from .core_cuda import inverse_rope_tile
                     target = scratch[:signal.numel()].view_as(signal)
-                    signal = inverse_rope_tile(signal, cosine[start:start+len(part)], sine[start:start+len(part)],
+                    signal = inverse_rope_tile(signal, cosine[start:start+n_part], sine[start:start+n_part],
                                                ctx.head_dim, target)
-                grad_low = low[:len(part), :ranks[index]]
+                grad_low = low[:n_part, :ranks[index]]
                 if dx is not None:
-                    bases[index].input_gradient(signal, a, b, dx[start:start+len(part)], grad_low, index > 0)
+                    bases[index].input_gradient(signal, a, b, dx[start:start+n_part], grad_low, index > 0)
                 else:
                     _low_rank(signal, b, grad_low, transpose=False)
-                inputs = (kept[index][start:start+len(part)] if kept else
-                          xa[:len(part), sum(ranks[:index]):sum(ranks[:index+1])])
+                inputs = (kept[index][start:start+n_part] if kept else
+                          xa[:n_part, sum(ranks[:index]):sum(ranks[:index+1])])
                 parameter_gradients(part, signal, *gradients[index], grad_low, inputs, add=start > 0)
         del bases, factors, stack
         results = [value for da, db in gradients for value in (None, da, db, None)]
