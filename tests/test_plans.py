@@ -60,7 +60,7 @@ def test_rank_r_product_splits(m, n, k, splits):
     (16, 6144, 24576, 0, 16),
     (16, 24576, 6144, 0, 4),
     (64, 24576, 6144, 1, 2),
-    (64, 6144, 24576, 1, 5),   # 96 column blocks: 5 x 96 = 480 workgroups, not 6 x 96 = 576
+    (64, 6144, 24576, 1, 8),   # 96 column blocks, 3 resident per CU: 8 x 96 = 768 workgroups, one round
     (64, 6144, 24576, 0, 5),   # 48 column blocks: 5 x 48 = 240, not 6 x 48 = 288
     (64, 24576, 6144, 0, 1),   # 192 column blocks: one round unsplit
 ])
