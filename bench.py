@@ -494,7 +494,8 @@ def epilogue_measure(device, rows=4096, reps=20, rank=R):
     projection call with its elementwise step in the library (fused into the GEMM or, where
     that measured slower, a pass right after it), against the same call without the step
     followed by the separate kernel the callers ran before (ct_rope, torch's add_,
-    ct_silu_multiply). Both sides compute the same bits."""
+    ct_silu_multiply; for SiLU x gate keeping up, the call writing the kept up and the kernel
+    reading it). Both sides compute the same bits."""
     from causal_tuner.kernels import _native
     from causal_tuner.kernels.core_cuda import _rope
     from causal_tuner.kernels.linear import _Base, _forward, _input_gradient
@@ -528,6 +529,7 @@ def epilogue_measure(device, rows=4096, reps=20, rank=R):
             plain = lambda: _input_gradient(dy, weight, bs.state, a, b, out, low, False)
             fused = lambda: _input_gradient(dy, weight, bs.state, a, b, out, low, False, epi)
             separate = lambda: _silu_kernel(gate, up, out, dg, du, backward=True, reconstruct=True)
+            keep_call = plain
         else:
             x = rnd(m, k)
             out, xa = torch.empty(m, n, device=device, dtype=torch.bfloat16), torch.empty(m, rank, device=device,
@@ -547,8 +549,14 @@ def epilogue_measure(device, rows=4096, reps=20, rank=R):
                 separate = lambda: _silu_kernel(gate, kept, out, None, None, backward=False, reconstruct=True)
             plain = lambda: _forward(x, weight, bs.state, a, b, None, out, xa)
             fused = lambda: _forward(x, weight, bs.state, a, b, None, out, xa, False, epi)
+            if kind == "silu":
+                # the caller's sequence keeps the raw up: the product goes to `kept`, then
+                # h = silu(gate) * up from it into `out`
+                keep_call = lambda: _forward(x, weight, bs.state, a, b, None, kept, xa)
+            else:
+                keep_call = plain
         def both():
-            plain()
+            keep_call()
             separate()
         # five interleaved rounds, the fastest of each: sides that run the same kernels (the
         # SiLU steps on 256 x 256 tiles take the separate pass) then differ by noise only
