@@ -107,3 +107,15 @@ def test_nf4_decode_first_thresholds(m, decoded_fwd, decoded_dx):
     weight = 24576 * 6144 * 2
     assert (lib.ct_forward_linear_workspace(m, 24576, 6144, 256, 1) >= weight) == decoded_fwd
     assert (lib.ct_input_gradient_workspace(m, 24576, 6144, 256, 1) >= weight) == decoded_dx
+
+
+def test_parameter_gradient_runs():
+    """Projections after the first share one dA/dB call when the cross products of their
+    dB^T stay under a tenth of the useful ones: k and v beside q (C3), not gate and up, not
+    three wide outputs."""
+    from causal_tuner.kernels.linear import param_run
+    assert param_run([256, 256, 256], [4096, 128, 128], 4096) == (1, 3)
+    assert param_run([256, 256], [11008, 11008], 4096) is None
+    assert param_run([256, 256, 256], [4096, 4096, 4096], 4096) is None
+    assert param_run([256, 128, 256], [4096, 128, 128], 4096) is None   # ranks differ
+    assert param_run([256, 256, 256], [2048, 128, 128], 2048) == (1, 3)   # C4's k and v
