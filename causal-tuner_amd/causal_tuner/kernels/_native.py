@@ -77,8 +77,8 @@ _SIGNATURES = {
     "ct_silu_multiply": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P]),
     "ct_rope": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P]),
     "ct_group_forward_workspace": (_I64, [_I64, _I32, _P, _I64, _I64]),
-    "ct_group_forward": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _I64,
-                                        _P]),
+    "ct_group_forward": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _P,
+                                        _I64, _P]),
     "ct_group_input_gradient_workspace": (_I64, [_I64, _I32, _P, _P, _I64]),
     "ct_group_input_gradient": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I64,
                                                _I64, _I32, _P, _I64, _P]),
@@ -107,7 +107,7 @@ EXPORTED = tuple(_SIGNATURES)
 _library = None
 
 
-ABI_VERSION = 11   # ct_abi_version() of the library these signatures describe
+ABI_VERSION = 12   # ct_abi_version() of the library these signatures describe
 
 
 def library_path():

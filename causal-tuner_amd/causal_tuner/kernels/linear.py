@@ -493,16 +493,16 @@ GROUP_FORWARD_ROWS = 512
 
 
 def group_forward_ready(bases, widths, ranks, rows, k, biases):
-    return (len(bases) == 2 and rows >= GROUP_FORWARD_ROWS and ranks[0] == ranks[1] > 0 and widths[0] % 256 == 0
-            and k % 8 == 0 and all(b is None for b in biases)
+    return (len(bases) == 2 and rows >= GROUP_FORWARD_ROWS and ranks[0] == ranks[1] > 0 and widths[0] % 64 == 0
+            and k % 8 == 0 and all(b is None or (b.dtype == torch.bfloat16 and b.is_contiguous()) for b in biases)
             and all(base.state is not None or (base.matrix.dtype == torch.bfloat16 and base.matrix.is_contiguous())
                     for base in bases))
 
 
-def group_forward(bases, x, b_stack, xa, outputs):
-    """out_i = x w_i^T + xa_i b_i^T for two projections that read x (forward_linear with the
-    stacked xa given, linear.py:72-86) as one GEMM over [w_1; w_2]: ct_group_forward. xa =
-    [xa_1 | xa_2]; `outputs` are written in place."""
+def group_forward(bases, x, b_stack, xa, outputs, biases=(None, None)):
+    """out_i = x w_i^T (+ bias_i) + xa_i b_i^T for two projections that read x (forward_linear
+    with the stacked xa given, linear.py:72-86) as one GEMM over [w_1; w_2]:
+    ct_group_forward. xa = [xa_1 | xa_2]; `outputs` are written in place."""
     m, k = x.shape
     x, ldx = _rows(x)
     xa, ldxa = _rows(xa)
@@ -513,13 +513,15 @@ def group_forward(bases, x, b_stack, xa, outputs):
     n_arr = (ctypes.c_int64 * 2)(*[out.shape[1] for out in outputs])
     out_arr = (ctypes.c_void_p * 2)(*[t.buffer.data_ptr() for t in targets])
     ld_arr = (ctypes.c_int64 * 2)(*[t.ld for t in targets])
+    bias_arr = None if all(b is None for b in biases) else \
+        (ctypes.c_void_p * 2)(*[None if b is None else _native.ptr(b) for b in biases])
     r = b_stack.shape[1]
     lib = _native.library()
     ws = _workspace(lib.ct_group_forward_workspace(m, 2, n_arr, k, r), x.device)
     with _native.device_of(x):
         status = lib.ct_group_forward(_native.ptr(x), ldx, 2, n_arr, dense, packed, _native.ptr(b_stack.contiguous()),
-                                      _native.ptr(xa), ldxa, out_arr, ld_arr, m, k, r, _native.ptr(ws), ws.numel(),
-                                      _native.stream_of(x))
+                                      _native.ptr(xa), ldxa, bias_arr, out_arr, ld_arr, m, k, r, _native.ptr(ws),
+                                      ws.numel(), _native.stream_of(x))
     _native.check(status, "ct_group_forward")
     for t in targets:
         t.finish()
@@ -696,13 +698,21 @@ class _LoRAGroup(torch.autograd.Function):
             fusable(*outputs[:rotated]) and all(out.shape[1] % head_dim == 0 for out in outputs[:rotated])
         residual_flat = None if residual is None else residual.reshape(total, -1)
         residual_fused = residual_flat is not None and not rotated and fusable(outputs[0], residual_flat)
-        # Two projections of one rank without biases or steps (gate and up) share one grid of
-        # output tiles from GROUP_FORWARD_ROWS rows: one partial last round instead of two.
+        # Two projections of one rank without steps (gate and up) share one grid of output
+        # tiles from GROUP_FORWARD_ROWS rows: one partial last round instead of two.
         paired = (stack is not None and not rotated and residual is None and x.is_cuda and dtype == torch.bfloat16
                   and group_forward_ready(bases, [out.shape[1] for out in outputs], ranks, span, flat.shape[1],
                                           biases))
         if paired:
             b_stack = stacked_rows([factors[1], factors[3]])
+        # Otherwise the last two of three (k and v beside q), when neither is rotated, share
+        # one grid the same way (C3: 2 x 128 columns as one grid of 64 x 64 tiles, 43 us
+        # instead of 71 us for two launches, measured on MI355X).
+        tail = (not paired and count == 3 and stack is not None and not rotated and x.is_cuda and dtype == torch.bfloat16
+                and group_forward_ready(bases[1:], [out.shape[1] for out in outputs[1:]], ranks[1:], span,
+                                        flat.shape[1], biases[1:]))
+        if tail:
+            tail_b = stacked_rows([factors[3], factors[5]])
         for start in range(0, total, step):
             part = flat[start:start+step]
             n_part = part.shape[0]
@@ -711,9 +721,13 @@ class _LoRAGroup(torch.autograd.Function):
             if stack is not None:
                 _low_rank(part, stack, xa[rows], transpose=True)
             if paired and n_part > 64:
-                group_forward(bases, part, b_stack, xa[rows], [out[window] for out in outputs])
+                group_forward(bases, part, b_stack, xa[rows], [out[window] for out in outputs], biases)
                 continue
             for index, base in enumerate(bases):
+                if tail and index == 1 and n_part > 64:
+                    group_forward(bases[1:], part, tail_b, xa[rows, ranks[0]:ranks[0] + ranks[1] + ranks[2]],
+                                  [out[window] for out in outputs[1:]], biases[1:])
+                    break
                 epilogue = None
                 if rope_fused and index < rotated:
                     epilogue = _native.epilogue(_native.CT_EPI_ROPE, n_part,

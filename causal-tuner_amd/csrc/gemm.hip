@@ -797,6 +797,9 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     void *cout = p.c;
     int64_t ldc = p.ldc;
     int64_t out_shift = second ? (int64_t)p.group_tiles * BN : 0;
+    // bias element of output column col: bias_p[col + bias_shift]
+    const uint16_t *bias_p = p.bias;
+    int64_t bias_shift = 0;
     Segment sg1;
     if (alt) {
         sg1 = p.seg[1];
@@ -804,6 +807,8 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
         cout = p.c_alt;
         ldc = p.ldc_alt;
         out_shift = -p.alt_col;
+        bias_p = p.bias_alt;
+        bias_shift = -p.alt_col;
     } else {
         sg1 = p.seg[1];
     }
@@ -856,7 +861,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
                 for (int j = 0; j < FN; ++j) {
                     const int64_t col = n0 + wn0 + 16 * j + (lane & 15);
                     if (col >= ncols) continue;
-                    const float bias = p.bias ? bf16_to_f32(p.bias[col]) : 0.f;
+                    const float bias = bias_p ? bf16_to_f32(bias_p[col + bias_shift]) : 0.f;
                     const float v = acc[i][j][e] + bias;
                     if constexpr (OUT == CT_F32) {
                         float *c = (second && p.c1) ? p.c1 + col * p.ldc1 + row
@@ -876,7 +881,8 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     const int64_t col = n0 + wn0 + (lane & 15) * FN;
     float bias[FN];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) bias[j] = (p.bias && col + j < ncols) ? bf16_to_f32(p.bias[col + j]) : 0.f;
+    for (int j = 0; j < FN; ++j)
+        bias[j] = (bias_p && col + j < ncols) ? bf16_to_f32(bias_p[col + j + bias_shift]) : 0.f;
     const bool full = col + FN <= ncols;
     if constexpr (OUT == CT_BF16) {
         if (p.epi.kind != CT_EPI_NONE && !p.beta) {
@@ -1649,7 +1655,7 @@ bool nf4_fusable(const ct_nf4_weight *w) {
 
 using namespace ct;
 
-extern "C" int ct_abi_version(void) { return 11; }
+extern "C" int ct_abi_version(void) { return 12; }
 
 extern "C" const char *ct_status_string(int status) {
     switch (status) {
@@ -1916,13 +1922,14 @@ extern "C" int64_t ct_group_forward_workspace(int64_t m, int32_t count, const in
 
 extern "C" int ct_group_forward(const void *x, int64_t ldx, int32_t count, const int64_t *n,
                                 const void *const *w_dense, const ct_nf4_weight *const *w_nf4, const void *b_stack,
-                                const void *xa, int64_t ldxa, void *const *out, const int64_t *ldo, int64_t m, int64_t k,
-                                int64_t r, void *workspace, int64_t workspace_bytes, hipStream_t stream) {
+                                const void *xa, int64_t ldxa, const void *const *bias, void *const *out,
+                                const int64_t *ldo, int64_t m, int64_t k, int64_t r, void *workspace,
+                                int64_t workspace_bytes, hipStream_t stream) {
     if (count != 2 || !n || !out || !ldo) return -CT_EINVAL_SHAPE;
     if (m < 0 || k < 0 || r < 0 || n[0] <= 0 || n[1] <= 0) return -CT_EINVAL_SHAPE;
     if (m == 0) return 0;
-    // the second projection starts on a tile boundary of every tile size (256)
-    if (n[0] % 256 || k % 8 || (r > 0 && ldxa < 2 * r)) return -CT_EINVAL_SHAPE;
+    // the second projection starts on a tile boundary (of the 64 x 64 tiles at least)
+    if (n[0] % 64 || k % 8 || (r > 0 && ldxa < 2 * r)) return -CT_EINVAL_SHAPE;
     if (!x || !out[0] || !out[1] || (r > 0 && (!xa || !b_stack))) return -CT_EINVAL_POINTER;
     if (ldx < k || ldo[0] < n[0] || ldo[1] < n[1]) return -CT_EINVAL_SHAPE;
     if (k == 0) return -CT_EINVAL_SHAPE;
@@ -1965,10 +1972,16 @@ extern "C" int ct_group_forward(const void *x, int64_t ldx, int32_t count, const
     pr.p.alt_a1 = r;
     pr.p.c_alt = out[1];
     pr.p.ldc_alt = ldo[1];
+    pr.p.bias = bias ? static_cast<const uint16_t *>(bias[0]) : nullptr;
+    pr.p.bias_alt = bias ? static_cast<const uint16_t *>(bias[1]) : nullptr;
     pr.src[0] = pr.src[1] = pr.src[2] = pr.src[3] = SRC_KC;
     pr.out = CT_BF16;
     pr.splits = 1;
-    pr.tile = -1;
+    // The tile the whole output would take, or the largest smaller one on whose edge the
+    // second projection starts.
+    int tile = choose_tile(m, nt, 1);
+    while (tile < TILE_64 && n[0] % kTileEdge[tile]) ++tile;
+    pr.tile = tile;
     // The few-row kernels do not take the column switch, and without a workspace the
     // split route is not taken: the tiled kernels only.
     if (m <= 64) return -CT_EINVAL_SHAPE;

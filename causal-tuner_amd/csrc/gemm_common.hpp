@@ -52,14 +52,16 @@ struct GemmParams {
     int64_t ldc1;
     // Elementwise step on a bf16 output (kind CT_EPI_NONE: none).
     EpiParams epi;
-    // Two projections side by side (ct_group_forward; alt_col > 0, a multiple of every tile
-    // edge): output columns from alt_col on belong to the second one, whose rank-r term
-    // reads segment 1's A operand alt_a1 elements further along its rows, and whose output
-    // goes to c_alt (ldc_alt) from its column 0. No elementwise step.
+    // Two projections side by side (ct_group_forward; alt_col > 0, a multiple of the
+    // launch's tile edge): output columns from alt_col on belong to the second one, whose
+    // rank-r term reads segment 1's A operand alt_a1 elements further along its rows, whose
+    // bias is bias_alt (bf16 [n - alt_col] or null) and whose output goes to c_alt (ldc_alt)
+    // from its column 0. No elementwise step.
     int64_t alt_col;
     int64_t alt_a1;
     void *c_alt;
     int64_t ldc_alt;
+    const uint16_t *bias_alt;
 };
 
 // ------------------------------------------------------------------ LDS layout and NF4 decode

@@ -352,23 +352,25 @@ int ct_forward_linear_static(const void *x, int64_t ldx,
 /*
  * Replaces the forward of two projections that read one input with one rank, when their
  * xa are given (the stacked x [a_1; a_2]^T of ct_gemm): forward_linear per projection in
- * _LoRAGroup.forward (kernels/linear.py:72-86) for gate and up. For i < 2:
- *   out_i = bf16(x w_i^T + xa[:, i r : (i + 1) r] b_i^T)        [m, n_i] (ldo[i])
+ * _LoRAGroup.forward (kernels/linear.py:72-86) for gate and up, or k and v beside q. For i < 2:
+ *   out_i = bf16(x w_i^T + bias_i + xa[:, i r : (i + 1) r] b_i^T)        [m, n_i] (ldo[i])
  * as one GEMM over [w_1; w_2] (n_1 + n_2 output columns), so the two share one grid of
- * tiles: one partial last round of 256 x 256 tiles instead of two. The results are those
- * of ct_forward_linear with xa_given per projection (the same products and sums). x [m, k]
+ * tiles: one partial last round instead of two. The results are those of
+ * ct_forward_linear with xa_given per projection (the same products and sums). x [m, k]
  * (ldx, k % 8 == 0), w_dense[i] bf16 [n_i, k] or w_nf4[i] (exactly one per projection),
- * b_stack bf16 [n_1 + n_2, r] = [b_1; b_2] (contiguous), xa [m, 2 r] (ldxa). n_1 is a
- * multiple of 256; no bias, no elementwise step. Needs m > 64 (-CT_EINVAL_SHAPE
- * otherwise: the caller runs the projections one by one); the reduction is never split.
+ * b_stack bf16 [n_1 + n_2, r] = [b_1; b_2] (contiguous), xa [m, 2 r] (ldxa), bias null or
+ * bias[i] bf16 [n_i] or null. n_1 is a multiple of 64; the grid takes the tile the whole
+ * output would take, or the largest smaller one whose edge divides n_1. No elementwise
+ * step. Needs m > 64 (-CT_EINVAL_SHAPE otherwise: the caller runs the projections one by
+ * one); the reduction is never split.
  * The weights are decoded (or copied) side by side into the workspace first, whose size
  * ct_group_forward_workspace gives (count must be 2).
  */
 int64_t ct_group_forward_workspace(int64_t m, int32_t count, const int64_t *n, int64_t k, int64_t r);
 int ct_group_forward(const void *x, int64_t ldx, int32_t count, const int64_t *n,
                      const void *const *w_dense, const ct_nf4_weight *const *w_nf4, const void *b_stack,
-                     const void *xa, int64_t ldxa, void *const *out, const int64_t *ldo, int64_t m, int64_t k,
-                     int64_t r, void *workspace, int64_t workspace_bytes, hipStream_t stream);
+                     const void *xa, int64_t ldxa, const void *const *bias, void *const *out, const int64_t *ldo,
+                     int64_t m, int64_t k, int64_t r, void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * Replaces input_gradient (kernels/linear.py:36-39):

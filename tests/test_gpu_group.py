@@ -162,23 +162,30 @@ def _workspace():
     return 5
 
 
-def _forward_single(x, weight, a, b, xa, m, n, k, r):
+def _forward_single(x, weight, a, b, xa, m, n, k, r, bias=None):
     lib = _native.library()
     out = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
     desc = None if isinstance(weight, torch.Tensor) else _native.nf4_descriptor(*weight)
     need = lib.ct_forward_linear_workspace(m, n, k, r, _native.nf4_kind(desc))
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
     status = lib.ct_forward_linear(x.data_ptr(), x.stride(0), weight.data_ptr() if desc is None else None, desc,
-                                   a.data_ptr(), b.data_ptr(), None, out.data_ptr(), n, xa.data_ptr(), xa.stride(0), 1,
+                                   a.data_ptr(), b.data_ptr(), None if bias is None else bias.data_ptr(),
+                                   out.data_ptr(), n, xa.data_ptr(), xa.stride(0), 1,
                                    m, n, k, r, None, ws.data_ptr(), ws.numel(), _native.stream_of(x))
     assert status == 0, status
     return out
 
 
-@pytest.mark.parametrize("m,k,widths,r,nf4", [(600, 256, (512, 256), 16, True), (520, 128, (256, 264), 8, False),
-                                              (8192, 512, (1024, 512), 64, True), (64, 128, (256, 256), 8, True)])
-def test_group_forward_matches_per_projection_forward(m, k, widths, r, nf4):
-    print(f"group forward: m={m} k={k} widths={widths} r={r} nf4={nf4}", flush=True)
+@pytest.mark.parametrize("m,k,widths,r,nf4,biased", [
+    (600, 256, (512, 256), 16, True, (False, False)), (520, 128, (256, 264), 8, False, (False, False)),
+    (8192, 512, (1024, 512), 64, True, (True, True)), (64, 128, (256, 256), 8, True, (False, False)),
+    # 256 x 256 tiles here and per projection, the first projection with a bias
+    (8192, 256, (2048, 2560), 16, True, (True, False)),
+    # narrow outputs (k and v beside q): 64 x 64 tiles, the second one with a bias
+    (8192, 512, (128, 128), 256, True, (True, True)), (600, 256, (192, 384), 16, True, (False, True)),
+    (333, 128, (384, 136), 8, False, (True, True))])
+def test_group_forward_matches_per_projection_forward(m, k, widths, r, nf4, biased):
+    print(f"group forward: m={m} k={k} widths={widths} r={r} nf4={nf4} biased={biased}", flush=True)
     lib = _native.library()
     x = _rand(m, k, seed=1)
     weights = []
@@ -189,6 +196,8 @@ def test_group_forward_matches_per_projection_forward(m, k, widths, r, nf4):
     b_stack = _rand(sum(widths), r, seed=6, scale=0.05)
     xa = _rand(m, 2 * r, seed=7)
     outs = [torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16) for n in widths]
+    biases = [_rand(n, seed=8 + i) if on else None for i, (n, on) in enumerate(zip(widths, biased))]
+    bias_arr = (ctypes.c_void_p * 2)(*[None if b is None else b.data_ptr() for b in biases]) if any(biased) else None
     n_arr = (ctypes.c_int64 * 2)(*widths)
     dense = (ctypes.c_void_p * 2)(*[w.data_ptr() if isinstance(w, torch.Tensor) else None for w in weights])
     descs = [None if isinstance(w, torch.Tensor) else _native.nf4_descriptor(*w) for w in weights]
@@ -198,7 +207,7 @@ def test_group_forward_matches_per_projection_forward(m, k, widths, r, nf4):
     need = lib.ct_group_forward_workspace(m, 2, n_arr, k, r)
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
     status = lib.ct_group_forward(x.data_ptr(), k, 2, n_arr, dense, packed, b_stack.data_ptr(), xa.data_ptr(), 2 * r,
-                                  out_arr, ld_arr, m, k, r, ws.data_ptr(), ws.numel(), _native.stream_of(x))
+                                  bias_arr, out_arr, ld_arr, m, k, r, ws.data_ptr(), ws.numel(), _native.stream_of(x))
     if m <= 64:
         assert status == -2   # few rows: the caller runs the projections one by one
         return
@@ -206,6 +215,6 @@ def test_group_forward_matches_per_projection_forward(m, k, widths, r, nf4):
     b_list = torch.split(b_stack, list(widths))
     for i, n in enumerate(widths):
         want = _forward_single(x, weights[i], a_stack[i * r:(i + 1) * r], b_list[i].contiguous(),
-                               xa[:, i * r:(i + 1) * r], m, n, k, r)
+                               xa[:, i * r:(i + 1) * r], m, n, k, r, biases[i])
         torch.cuda.synchronize()
         assert torch.equal(outs[i].view(torch.int16), want.view(torch.int16)), i
