@@ -1434,6 +1434,29 @@ bool epilogue_fused(const Problem &pr) {
     return !(tile == TILE_256 && (p.epi.kind == CT_EPI_SILU || p.epi.kind == CT_EPI_DSILU));
 }
 
+// A 256 x 256 grid whose last round holds at most half of the 256 CUs' workgroups (C3's
+// dx of down: 32 x 43 tiles, 5 rounds and 96 tiles) splits its output columns: the first
+// `head` (a multiple of 256) give whole rounds, the rest (at most 128 tiles' worth) run as
+// a second launch of 128 x 128 tiles, two per CU. Dense bf16 operands with plain bf16
+// output only: the B operands and the output are offset by `head` columns.
+bool column_split(const Problem &pr, int64_t *head) {
+    const GemmParams &p = pr.p;
+    if (pr.splits != 1 || pr.out != CT_BF16 || p.group_tiles > 0 || p.alt_col > 0 || p.epi.kind != CT_EPI_NONE)
+        return false;
+    for (int s = 0; s < p.nseg; ++s) {
+        const int a = pr.src[2 * s], b = pr.src[2 * s + 1];
+        if (a != SRC_KC || (b != SRC_KC && b != SRC_KS)) return false;
+    }
+    const int64_t tm = cdiv(p.m, 256), tn = cdiv(p.n, 256);
+    const int64_t rem = (tm * tn) % 256;
+    if (rem == 0 || rem > 128 || tn < 2) return false;
+    int64_t lead = tn - 1;
+    while (lead > 0 && (tm * lead) % 256) --lead;
+    if (lead <= 0 || tm * (tn - lead) > 128) return false;
+    *head = lead * 256;
+    return true;
+}
+
 hipError_t run(Problem &pr, hipStream_t s) {
     GemmParams &p = pr.p;
     if (p.m == 0 || p.n == 0) return hipSuccess;
@@ -1496,6 +1519,27 @@ hipError_t run(Problem &pr, hipStream_t s) {
         }
     }
     const int tile = pr.tile >= 0 ? pr.tile : choose_tile(p.m, p.n, pr.splits);
+    if (pr.tile < 0 && tile == TILE_256) {
+        int64_t head = 0;
+        if (column_split(pr, &head)) {
+            // The leading columns on 256 x 256 tiles in whole rounds, the rest on the tile
+            // their own width takes: the same per-element sums either way.
+            Problem lead = pr, rest = pr;
+            lead.p.n = head;
+            lead.tile = TILE_256;
+            rest.p.n = p.n - head;
+            rest.p.c = static_cast<uint16_t *>(p.c) + head;
+            rest.ws = nullptr;  // unsplit, as the whole grid would run
+            rest.ws_bytes = 0;
+            if (p.bias) rest.p.bias = p.bias + head;
+            for (int g = 0; g < p.nseg; ++g) {
+                Operand &b = rest.p.seg[g].b;
+                b.p = static_cast<const uint16_t *>(b.p) + (pr.src[2 * g + 1] == SRC_KC ? head * b.ld : head);
+            }
+            const hipError_t e = run(lead, s);
+            return e != hipSuccess ? e : run(rest, s);
+        }
+    }
     const int64_t tiles = total_tiles(p);
     p.tiles_per_split = cdiv(tiles > 0 ? tiles : 1, pr.splits);
     const bool nf4 = is_nf4_host(pr.src[0]) || is_nf4_host(pr.src[1]);

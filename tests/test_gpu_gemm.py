@@ -190,3 +190,63 @@ def test_split_route_with_bias_and_accumulation(m, n, k):
                        None, 1, m, n, k, ws.data_ptr(), need, _native.stream_of(c)) == 0
     worst, norm = _err(c, first.double() + product)
     assert worst <= 8e-3 and norm <= 4e-3, (worst, norm)
+
+
+@pytest.mark.parametrize("trans_b", [0, 1])
+def test_partial_last_round_column_split_matches_row_slices(trans_b):
+    """8192 x 11008 on 256 x 256 tiles is 5 whole rounds of the 256 CUs and 96 tiles: the
+    first 10240 columns run as the whole rounds and the last 768 as a second launch on
+    128 x 128 tiles (C3's dx of down has this output). Every element's sum is the one a
+    256-row slice computes alone (on 64 x 64 tiles, one launch), bit for bit, and the
+    float64 product of the same operands bounds both."""
+    lib = _native.library()
+    m, n, k = 8192, 11008, 320
+    a, abase, lda = _operand(m, k, False)
+    b, bbase, ldb = _operand(k, n, bool(trans_b))
+    bias = (torch.randn(n, device="cuda") * 0.5).to(torch.bfloat16)
+    c = torch.full((m, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+    assert lib.ct_gemm(abase.data_ptr(), lda, 0, bbase.data_ptr(), ldb, trans_b, c.data_ptr(), n, _native.CT_BF16,
+                       bias.data_ptr(), 0, m, n, k, None, 0, _native.stream_of(c)) == 0
+    for start in (0, m - 256):
+        part = torch.full((256, n), float("nan"), device="cuda", dtype=torch.bfloat16)
+        assert lib.ct_gemm(abase[start:].data_ptr(), lda, 0, bbase.data_ptr(), ldb, trans_b, part.data_ptr(), n,
+                           _native.CT_BF16, bias.data_ptr(), 0, 256, n, k, None, 0, _native.stream_of(c)) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(c[start:start + 256].view(torch.int16), part.view(torch.int16)), start
+    want = a.double() @ b.double() + bias.double()
+    worst, norm = _err(c, want)
+    assert worst <= 8e-3 and norm <= 4e-3, (worst, norm)
+
+
+def test_partial_last_round_column_split_in_the_input_gradient():
+    """dx = [dy | low] [w ; a] at C3's down shape (8192 x 11008 output, dense weight): the
+    column split offsets both segments' B operands; each 256-row slice computed alone gives
+    the same bits."""
+    lib = _native.library()
+    m, n, k, r = 8192, 192, 11008, 32
+    g = torch.Generator(device="cuda").manual_seed(3)
+    dy = torch.randn(m, n, device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+    a = (torch.randn(r, k, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+    bf = (torch.randn(n, r, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+
+    def call(rows, start):
+        dx = torch.full((rows, k), float("nan"), device="cuda", dtype=torch.bfloat16)
+        low = torch.empty(rows, r, device="cuda", dtype=torch.bfloat16)
+        need = lib.ct_input_gradient_workspace(rows, n, k, r, 0)
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+        assert lib.ct_input_gradient(dy[start:].data_ptr(), n, w.data_ptr(), None, a.data_ptr(), bf.data_ptr(),
+                                     dx.data_ptr(), k, low.data_ptr(), rows, n, k, r, 0, None,
+                                     ws.data_ptr() if rows > 256 else None, need if rows > 256 else 0,
+                                     _native.stream_of(dx)) == 0
+        return dx
+
+    full = call(m, 0)
+    for start in (0, m - 256):
+        part = call(256, start)
+        torch.cuda.synchronize()
+        assert torch.equal(full[start:start + 256].view(torch.int16), part.view(torch.int16)), start
+    low = (dy.double() @ bf.double()).bfloat16().double()
+    want = dy.double() @ w.double() + low @ a.double()
+    worst, norm = _err(full, want)
+    assert worst <= 8e-3 and norm <= 4e-3, (worst, norm)
