@@ -37,6 +37,7 @@ import argparse
 import csv
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -495,7 +496,8 @@ def epilogue_measure(device, rows=4096, reps=20, rank=R):
     that measured slower, a pass right after it), against the same call without the step
     followed by the separate kernel the callers ran before (ct_rope, torch's add_,
     ct_silu_multiply; for SiLU x gate keeping up, the call writing the kept up and the kernel
-    reading it). Both sides compute the same bits."""
+    reading it). Both sides compute the same bits. `saved_us` is the median over the rounds
+    of (call + separate kernel) - (call with its step), each pair measured in one round."""
     from causal_tuner.kernels import _native
     from causal_tuner.kernels.core_cuda import _rope
     from causal_tuner.kernels.linear import _Base, _forward, _input_gradient
@@ -558,16 +560,20 @@ def epilogue_measure(device, rows=4096, reps=20, rank=R):
         def both():
             keep_call()
             separate()
-        # five interleaved rounds, the fastest of each: sides that run the same kernels (the
-        # SiLU steps on 256 x 256 tiles take the separate pass) then differ by noise only
+        # nine interleaved rounds, each side in each position of a round three times; the
+        # times are the fastest of each side, the saving the median of the rounds' paired
+        # differences (sides that run the same kernels, as the SiLU steps on 256 x 256 tiles
+        # do through the separate pass, then differ by the noise of one round only)
         times = {"plain": [], "fused": [], "both": []}
-        for _ in range(5):
-            for key, fn in (("plain", plain), ("fused", fused), ("both", both)):
+        sides = (("plain", plain), ("fused", fused), ("both", both))
+        for round_ in range(9):
+            for key, fn in sides[round_ % 3:] + sides[:round_ % 3]:
                 times[key].append(_events_us(fn, reps))
         t_plain, t_fused, t_both = (min(times[key]) for key in ("plain", "fused", "both"))
+        saved = statistics.median(b - f for b, f in zip(times["both"], times["fused"]))
         results[name] = {"rows": m, "in": k, "out": n, "call_us": round(t_plain, 1),
                          "with_step_us": round(t_fused, 1), "call_then_separate_us": round(t_both, 1),
-                         "saved_us": round(t_both - t_fused, 1)}
+                         "saved_us": round(saved, 1)}
         log(f"  {name:17s} call {t_plain:7.1f} us | with its step {t_fused:7.1f} us | "
             f"call + separate kernel {t_both:7.1f} us")
         del bs, a, b, out
