@@ -216,6 +216,15 @@ def test_partial_last_round_column_split_matches_row_slices(trans_b):
     want = a.double() @ b.double() + bias.double()
     worst, norm = _err(c, want)
     assert worst <= 8e-3 and norm <= 4e-3, (worst, norm)
+    # beta accumulation into a pitched output (row pitch past n), on both launches
+    ld = n + 64
+    d = torch.full((m, ld), float("nan"), device="cuda", dtype=torch.bfloat16)
+    d[:, :n] = c
+    assert lib.ct_gemm(abase.data_ptr(), lda, 0, bbase.data_ptr(), ldb, trans_b, d.data_ptr(), ld, _native.CT_BF16,
+                       None, 1, m, n, k, None, 0, _native.stream_of(d)) == 0
+    worst, norm = _err(d[:, :n], c.double() + a.double() @ b.double())
+    assert worst <= 8e-3 and norm <= 4e-3, (worst, norm)
+    assert torch.isnan(d[:, n:]).all()
 
 
 def test_partial_last_round_column_split_in_the_input_gradient():
