@@ -212,6 +212,8 @@ def cast_all(tensors, dtype, outputs=None):
             out[i] = outputs[i]
             if out[i] is None:
                 fresh.append(i)
+        # fresh outputs are consecutive views of one buffer, so factors cast together can be
+        # stacked without a copy (stacked_rows)
         sizes = [tensors[i].numel() for i in fresh]
         buffer = torch.empty(sum((n + 7) // 8 * 8 for n in sizes), dtype=torch.bfloat16, device=first.device)
         offset = 0
@@ -448,9 +450,10 @@ def stacked_rows(tensors):
     """[t_1; t_2; ...] for contiguous matrices of one width: a view when they are consecutive
     rows of one buffer (the stacked factors group_factors casts into), else a copy."""
     first = tensors[0]
-    width, offset = first.shape[1], first.data_ptr()
+    width, offset, storage = first.shape[1], first.data_ptr(), first.untyped_storage().data_ptr()
     for t in tensors:
-        if not t.is_contiguous() or t.shape[1] != width or t.data_ptr() != offset:
+        if (not t.is_contiguous() or t.shape[1] != width or t.data_ptr() != offset
+                or t.untyped_storage().data_ptr() != storage):
             return torch.cat(tensors)
         offset += t.numel() * t.element_size()
     return first.as_strided((sum(t.shape[0] for t in tensors), width), (width, 1))
@@ -643,10 +646,11 @@ def param_run(ranks, widths, k):
 def _adjacent(views):
     """One view over column slices of one matrix that follow each other, or None."""
     first = views[0]
-    element = first.element_size()
+    element, storage = first.element_size(), first.untyped_storage().data_ptr()
     offset = 0
     for view in views:
-        if view.stride() != first.stride() or view.data_ptr() != first.data_ptr() + offset * element:
+        if (view.stride() != first.stride() or view.data_ptr() != first.data_ptr() + offset * element
+                or view.untyped_storage().data_ptr() != storage):
             return None
         offset += view.shape[1]
     return first.as_strided((first.shape[0], offset), first.stride())
@@ -667,7 +671,7 @@ class _LoRAGroup(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, dtype, tile, states, cosine, sine, head_dim, residual, *parameters):
         count = len(states)
-        flat = x.reshape(-1, x.shape[-1]).to(dtype)
+        flat = _matrix_of(x).to(dtype)
         total = flat.shape[0]
         element = dtype.itemsize
         step, keep = _plan_rows(total, tile, _KEEP_BUDGET.get(),
@@ -682,7 +686,7 @@ class _LoRAGroup(torch.autograd.Function):
         # xa of every projection for the rows of one tile (all rows when kept), as column
         # slices of one buffer so a stacked GEMM fills them together.
         xa = torch.empty((total if keep else span, sum(ranks)), device=x.device, dtype=dtype)
-        columns = [xa[:, sum(ranks[:i]):sum(ranks[:i+1])] for i in range(count)]
+        columns = [xa] if count == 1 else [xa[:, sum(ranks[:i]):sum(ranks[:i+1])] for i in range(count)]
         # The rotation of q/k (core_cuda.py:192-200) and the residual add (linear.py:90-91)
         # run in the GEMM epilogue when the operands allow it, else as separate passes.
         rotated = min(count, 2) if head_dim else 0
@@ -713,20 +717,22 @@ class _LoRAGroup(torch.autograd.Function):
                                         flat.shape[1], biases[1:]))
         if tail:
             tail_b = stacked_rows([factors[3], factors[5]])
+        whole = step >= total   # one tile over every row: the tensors themselves, no row views
         for start in range(0, total, step):
-            part = flat[start:start+step]
+            part = _cut(flat, slice(start, start+step), whole)
             n_part = part.shape[0]
             rows = slice(start, start+n_part) if keep else slice(0, n_part)
             window = slice(start, start+n_part)
             if stack is not None:
-                _low_rank(part, stack, xa[rows], transpose=True)
+                _low_rank(part, stack, _cut(xa, rows, whole), transpose=True)
             if paired and n_part > 64:
-                group_forward(bases, part, b_stack, xa[rows], [out[window] for out in outputs], biases)
+                group_forward(bases, part, b_stack, _cut(xa, rows, whole), [_cut(out, window, whole) for out in outputs],
+                              biases)
                 continue
             for index, base in enumerate(bases):
                 if tail and index == 1 and n_part > 64:
                     group_forward(bases[1:], part, tail_b, xa[rows, ranks[0]:ranks[0] + ranks[1] + ranks[2]],
-                                  [out[window] for out in outputs[1:]], biases[1:])
+                                  [_cut(out, window, whole) for out in outputs[1:]], biases[1:])
                     break
                 epilogue = None
                 if rope_fused and index < rotated:
@@ -734,15 +740,17 @@ class _LoRAGroup(torch.autograd.Function):
                                                 rotary=(trig[0][window], trig[1][window], head_dim))
                 elif residual_fused and index == 0:
                     epilogue = _native.epilogue(_native.CT_EPI_RESIDUAL, n_part, in0=residual_flat[window])
-                base.forward(part, factors[2*index], factors[2*index+1], biases[index], outputs[index][window],
-                             columns[index][rows], xa_given=stack is not None, epilogue=epilogue)
+                base.forward(part, factors[2*index], factors[2*index+1], biases[index],
+                             _cut(outputs[index], window, whole), _cut(columns[index], rows, whole),
+                             xa_given=stack is not None, epilogue=epilogue)
         # Under a projection budget the backward also reuses the compute-dtype factors
         # (the reference casts them again, linear.py:108: the same values).
         kept = [*columns, *factors] if keep else []
         ctx.kept = len(kept)
         ctx.save_for_backward(x, cosine, sine, *parameters, *kept)
         del factors, stack, bases, xa, columns, kept
-        outputs = [out.reshape(*x.shape[:-1], out.shape[1]) for out in outputs]
+        if x.dim() != 2:
+            outputs = [out.reshape(*x.shape[:-1], out.shape[1]) for out in outputs]
         if rotated and not rope_fused:
             from .core_cuda import rotate_owned_qk
             rotate_owned_qk(outputs[0], outputs[1], cosine, sine, head_dim)
@@ -756,7 +764,7 @@ class _LoRAGroup(torch.autograd.Function):
         count = len(ctx.states)
         parameters, kept = rest[:4*count], rest[4*count:4*count+count]
         saved_factors = rest[4*count+count:]
-        flat = x.reshape(-1, x.shape[-1]).to(ctx.dtype)
+        flat = _matrix_of(x).to(ctx.dtype)
         total = flat.shape[0]
         dx = torch.empty_like(flat) if ctx.needs_input_grad[0] else None
         if ctx.head_dim:
@@ -769,7 +777,7 @@ class _LoRAGroup(torch.autograd.Function):
         bases = [_Base(parameters[4*i], state, ctx.dtype) if dx is not None else None
                  for i, state in enumerate(ctx.states)]
         ranks = [parameters[4*i+1].shape[0] for i in range(count)]
-        signals = [grad.reshape(-1, grad.shape[-1]).to(ctx.dtype) for grad in grad_outputs]
+        signals = [_matrix_of(grad).to(ctx.dtype) for grad in grad_outputs]
         allocate = torch.empty_like if total else torch.zeros_like
         gradients = [(allocate(parameters[4*i+1]), allocate(parameters[4*i+2])) for i in range(count)]
         xa = None if kept else torch.empty((span, sum(ranks)), device=x.device, dtype=ctx.dtype)
@@ -807,8 +815,9 @@ class _LoRAGroup(torch.autograd.Function):
             n_lo, n_hi = sum(widths[:run[0]]), sum(widths[:run[1]])
             run_da = torch.empty((r_hi - r_lo, flat.shape[1]), device=x.device, dtype=gradients[0][0].dtype)
             run_db = torch.empty((n_hi - n_lo, r_hi - r_lo), device=x.device, dtype=gradients[0][1].dtype)
+        whole = step >= total   # one tile over every row: the tensors themselves, no row views
         for start in range(0, total, step):
-            part = flat[start:start+step]
+            part = _cut(flat, slice(start, start+step), whole)
             n_part = part.shape[0]
             if not kept:
                 if stack is not None:
@@ -843,20 +852,20 @@ class _LoRAGroup(torch.autograd.Function):
                     parameter_gradients(part, joined[:n_part, n_lo:n_hi], run_da, run_db, low[:n_part, r_lo:r_hi],
                                         inputs, add=start > 0)
                 continue
+            window = slice(start, start+n_part)
             for index in range(count):
                 a, b = factors[2*index], factors[2*index+1]
-                signal = signals[index][start:start+n_part]
+                signal = _cut(signals[index], window, whole)
                 if index < rotated:
                     from .core_cuda import inverse_rope_tile
                     target = scratch[:signal.numel()].view_as(signal)
-                    signal = inverse_rope_tile(signal, cosine[start:start+n_part], sine[start:start+n_part],
-                                               ctx.head_dim, target)
-                grad_low = low[:n_part, :ranks[index]]
+                    signal = inverse_rope_tile(signal, cosine[window], sine[window], ctx.head_dim, target)
+                grad_low = low if whole and low.shape[1] == ranks[index] else low[:n_part, :ranks[index]]
                 if dx is not None:
-                    bases[index].input_gradient(signal, a, b, dx[start:start+n_part], grad_low, index > 0)
+                    bases[index].input_gradient(signal, a, b, _cut(dx, window, whole), grad_low, index > 0)
                 else:
                     _low_rank(signal, b, grad_low, transpose=False)
-                inputs = (kept[index][start:start+n_part] if kept else
+                inputs = (_cut(kept[index], window, whole) if kept else
                           xa[:n_part, sum(ranks[:index]):sum(ranks[:index+1])])
                 parameter_gradients(part, signal, *gradients[index], grad_low, inputs, add=start > 0)
         if run is not None:
@@ -868,8 +877,20 @@ class _LoRAGroup(torch.autograd.Function):
         del bases, factors, stack
         results = [value for da, db in gradients for value in (None, da, db, None)]
         residual_grad = grad_outputs[0] if ctx.needs_input_grad[7] else None
-        return (None if dx is None else dx.reshape_as(x).to(x.dtype), None, None, None, None, None, None,
+        if dx is not None and x.dim() != 2:
+            dx = dx.reshape_as(x)
+        return (None if dx is None else dx.to(x.dtype), None, None, None, None, None, None,
                 residual_grad, *results)
+
+
+def _matrix_of(t):
+    """t as [rows, last dimension] (itself when it is a matrix already)."""
+    return t if t.dim() == 2 else t.reshape(-1, t.shape[-1])
+
+
+def _cut(t, rows, whole):
+    """t[rows], or t itself when one tile spans all of its rows (saves a view per call)."""
+    return t if whole else t[rows]
 
 
 def _low_rank(x, factor, out, *, transpose):
