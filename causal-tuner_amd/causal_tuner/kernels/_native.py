@@ -247,14 +247,20 @@ def nf4_descriptor(weight, state):
 
 def nf4_fused_supported(weight, state):
     """ct_nf4_fused_supported of the weight's descriptor, kept beside the descriptor."""
+    return nf4_fused_descriptor(weight, state) is not None
+
+
+def nf4_fused_descriptor(weight, state):
+    """The weight's descriptor when the fused loaders take it (ct_nf4_fused_supported, kept
+    beside the descriptor), else None."""
     desc = nf4_descriptor(weight, state)
     cached = getattr(state, "_ct_descriptor", None)
     if cached is not None and cached[1] is desc and cached[2] is not None:
-        return cached[2]
+        return desc if cached[2] else None
     supported = library().ct_nf4_fused_supported(desc) == 1
     if cached is not None and cached[1] is desc:
         state._ct_descriptor = (cached[0], desc, supported)
-    return supported
+    return desc if supported else None
 
 
 def _build_nf4_descriptor(weight, state):

@@ -323,10 +323,11 @@ def forward_linear(x, weight, a, b, *, out, xa, bias=None):
     _forward(x, weight, None, a, b, bias, out, xa)
 
 
-def _forward(x, weight, state, a, b, bias, out, xa, xa_given=False, epilogue=None):
+def _forward(x, weight, state, a, b, bias, out, xa, xa_given=False, epilogue=None, desc=None):
     """ct_forward_linear; with xa_given, xa (a row-major view, e.g. a column slice of a
     group's shared x [a_1; a_2; ...]^T) already holds x a^T and is only read. `epilogue`
-    (a _native.Epilogue over `out`'s rows) is applied to the output in the GEMM."""
+    (a _native.Epilogue over `out`'s rows) is applied to the output in the GEMM. `desc` is the
+    weight's NF4 descriptor when the caller holds it already."""
     m, k = x.shape
     n, r = out.shape[1], a.shape[0]
     x, ldx = _rows(x)
@@ -338,7 +339,8 @@ def _forward(x, weight, state, a, b, bias, out, xa, xa_given=False, epilogue=Non
         raise ValueError("a fused epilogue needs a unit-stride, 16-byte aligned output")
     if xa_given and low.buffer is not xa:
         low.buffer.copy_(xa)
-    desc = None if state is None else _native.nf4_descriptor(w, state)
+    if state is not None and desc is None:
+        desc = _native.nf4_descriptor(w, state)
     lib = _native.library()
     ws = _workspace(_query("ct_forward_linear_workspace", m, n, k, r, _native.nf4_kind(desc)), x.device)
     with _native.device_of(x):
@@ -373,7 +375,7 @@ def input_gradient(dy, weight, a, b, dx, low, *, add=False):
     _input_gradient(dy, weight, None, a, b, dx, low, add)
 
 
-def _input_gradient(dy, weight, state, a, b, dx, low, add, epilogue=None):
+def _input_gradient(dy, weight, state, a, b, dx, low, add, epilogue=None, desc=None):
     m, n = dy.shape
     k, r = dx.shape[1], a.shape[0]
     dy, lddy = _rows(dy)
@@ -384,7 +386,8 @@ def _input_gradient(dy, weight, state, a, b, dx, low, add, epilogue=None):
         raise ValueError("a fused epilogue needs add=False and a unit-stride, 16-byte aligned dx")
     if add and target.buffer is not dx:
         target.buffer.copy_(dx)
-    desc = None if state is None else _native.nf4_descriptor(w, state)
+    if state is not None and desc is None:
+        desc = _native.nf4_descriptor(w, state)
     lib = _native.library()
     ws = _workspace(_query("ct_input_gradient_workspace", m, n, k, r, _native.nf4_kind(desc)), dy.device)
     with _native.device_of(dy):
@@ -473,7 +476,7 @@ def group_input_gradient(bases, dy, widths, ranks, a_stack, bs, dx, low, add):
     target = _Output(dx)
     if add and target.buffer is not dx:
         target.buffer.copy_(dx)
-    descs = [None if base.state is None else _native.nf4_descriptor(base.weight, base.state) for base in bases]
+    descs = [base.desc if base.state is not None else None for base in bases]
     dense = (ctypes.c_void_p * count)(*[None if d is not None else base.matrix.data_ptr()
                                         for base, d in zip(bases, descs)])
     packed = (ctypes.POINTER(_native.NF4Weight) * count)(*[None if d is None else ctypes.pointer(d) for d in descs])
@@ -510,7 +513,7 @@ def group_forward(bases, x, b_stack, xa, outputs, biases=(None, None)):
     x, ldx = _rows(x)
     xa, ldxa = _rows(xa)
     targets = [_Output(out) for out in outputs]
-    descs = [None if base.state is None else _native.nf4_descriptor(base.weight, base.state) for base in bases]
+    descs = [base.desc if base.state is not None else None for base in bases]
     dense = (ctypes.c_void_p * 2)(*[None if d is not None else base.matrix.data_ptr() for base, d in zip(bases, descs)])
     packed = (ctypes.POINTER(_native.NF4Weight) * 2)(*[None if d is None else ctypes.pointer(d) for d in descs])
     n_arr = (ctypes.c_int64 * 2)(*[out.shape[1] for out in outputs])
@@ -554,10 +557,11 @@ class _Base:
     """
 
     def __init__(self, weight, state, dtype):
-        self.weight, self.state, self.matrix = weight, None, None
+        self.weight, self.state, self.matrix, self.desc = weight, None, None, None
         if state is not None and weight.is_cuda and dtype == torch.bfloat16 and weight.dtype == torch.uint8 \
                 and weight.is_contiguous() and state.quant_type == "nf4":
-            if _native.nf4_fused_supported(weight, state):
+            self.desc = _native.nf4_fused_descriptor(weight, state)
+            if self.desc is not None:
                 self.state = state
         if self.state is None:
             self.matrix = materialize(weight, state, dtype)
@@ -568,20 +572,20 @@ class _Base:
         already; `epilogue` is an elementwise step fused into the output."""
         if xa_given or epilogue is not None:
             _forward(x, self.matrix if self.state is None else self.weight, self.state, a, b, bias, out, xa,
-                     xa_given, epilogue)
+                     xa_given, epilogue, self.desc)
         elif self.state is None:
             forward_linear(x, self.matrix, a, b, bias=bias, out=out, xa=xa)
         else:
-            _forward(x, self.weight, self.state, a, b, bias, out, xa)
+            _forward(x, self.weight, self.state, a, b, bias, out, xa, desc=self.desc)
 
     def input_gradient(self, dy, a, b, dx, low, add, epilogue=None):
         if epilogue is not None:
             _input_gradient(dy, self.matrix if self.state is None else self.weight, self.state, a, b, dx, low, add,
-                            epilogue)
+                            epilogue, self.desc)
         elif self.state is None:
             input_gradient(dy, self.matrix, a, b, dx, low, add=add)
         else:
-            _input_gradient(dy, self.weight, self.state, a, b, dx, low, add)
+            _input_gradient(dy, self.weight, self.state, a, b, dx, low, add, desc=self.desc)
 
 
 # Rows per tile of a projection group called without a tile: the reference's bound
@@ -747,6 +751,8 @@ class _LoRAGroup(torch.autograd.Function):
         # (the reference casts them again, linear.py:108: the same values).
         kept = [*columns, *factors] if keep else []
         ctx.kept = len(kept)
+        # bases that hold no decoded copy (packed NF4 for the fused loaders) serve the backward too
+        ctx.bases = bases if all(base.matrix is None for base in bases) else None
         ctx.save_for_backward(x, cosine, sine, *parameters, *kept)
         del factors, stack, bases, xa, columns, kept
         if x.dim() != 2:
@@ -774,8 +780,12 @@ class _LoRAGroup(torch.autograd.Function):
             factors, stack = list(saved_factors), None
         else:
             factors, stack = group_factors(parameters, count, ctx.dtype, x)
-        bases = [_Base(parameters[4*i], state, ctx.dtype) if dx is not None else None
-                 for i, state in enumerate(ctx.states)]
+        if dx is None:
+            bases = [None] * count
+        elif ctx.bases is not None:
+            bases = ctx.bases
+        else:
+            bases = [_Base(parameters[4*i], state, ctx.dtype) for i, state in enumerate(ctx.states)]
         ranks = [parameters[4*i+1].shape[0] for i in range(count)]
         signals = [_matrix_of(grad).to(ctx.dtype) for grad in grad_outputs]
         allocate = torch.empty_like if total else torch.zeros_like
