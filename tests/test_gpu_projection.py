@@ -260,7 +260,9 @@ def test_c3_projection_against_fp32_torch_reference(name, k, n):
 
 @pytest.mark.parametrize("m,n,k,r", [(8192, 4096, 4096, 256), (2048, 128, 4096, 256), (4096, 11008, 4096, 256),
                                      (300, 40, 72, 5), (777, 200, 136, 64), (520, 96, 0, 16), (520, 0, 96, 16),
-                                     (4096, 264, 520, 40)])
+                                     (4096, 264, 520, 40),
+                                     # ranks up to 64 over at most 512 tokens: one direct 128 x 128 grid
+                                     (512, 1024, 1024, 16), (256, 264, 520, 64), (16, 128, 256, 8)])
 def test_parameter_gradients_grouped_launch(m, n, k, r):
     """dA = low^T x and dB = dy^T xa (kernels/linear.py:42-44) from one grouped launch with a
     split token reduction: fp32 results against float64 on the host, NaN-filled outputs
