@@ -187,7 +187,8 @@ def skinny_bytes(m, k, n, r):
 def projection_measure(device, shapes, rows_list, iters=20, rank=R):
     """One NF4-LoRA projection fwd+bwd through project_group + autograd (the reference's
     operator path), per shape and row count: average ms over `iters` back-to-back steps
-    (HIP events; the rates use it), the GPU's own time per step (the steps queued behind
+    after 3 untimed ones (200 after 20 up to 512 rows, where the step is short and
+    host-bound; HIP events; the rates use it), the GPU's own time per step (the steps queued behind
     a spin kernel, so host-side work is hidden), algorithmic TFLOP/s and GB/s, and the
     fraction of the bound that applies (HBM for few rows, bf16 MFMA for many). Under the
     C3 step's projection budget, as there.
@@ -212,12 +213,15 @@ def projection_measure(device, shapes, rows_list, iters=20, rank=R):
                 with projection_budget(PROJECTION_BUDGET):
                     out, = project_group((module,), x)
                 torch.autograd.grad(out, (x, module.lora_A, module.lora_B), dy)
+            # few-row steps are host-bound and short: more steps after a longer warm-up (the
+            # first calls on a new shape build its descriptors and workspaces)
+            reps, warm = (max(iters, 200), 20) if m <= 512 else (iters, 3)
             with torch.autograd.set_multithreading_enabled(False):
-                ms = time_events(step, iters)
-            ms_engine = time_events(step, iters)
+                ms = time_events(step, reps, warm)
+            ms_engine = time_events(step, reps, warm)
             # the same steps queued behind a spin kernel: the GPU's own time per step, which
             # the host-side operator path (autograd, ctypes calls) hides at few rows
-            gpu_ms = _events_us(step, iters) * 1e-3
+            gpu_ms = _events_us(step, reps) * 1e-3
             flops, nbytes = projection_flops(m, k, n, rank), skinny_bytes(m, k, n, rank)
             tflops, gbs = flops / (ms * 1e-3) / 1e12, nbytes / (ms * 1e-3) / 1e9
             bound = "hbm" if flops / nbytes < BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma"
