@@ -1974,6 +1974,9 @@ extern "C" int ct_group_forward(const void *x, int64_t ldx, int32_t count, const
     if (m == 0) return 0;
     // the second projection starts on a tile boundary (of the 64 x 64 tiles at least)
     if (n[0] % 64 || k % 8 || (r > 0 && ldxa < 2 * r)) return -CT_EINVAL_SHAPE;
+    // The few-row kernels do not take the column switch: the caller runs the projections
+    // one by one (refused before any work is queued).
+    if (m <= 64) return -CT_EINVAL_SHAPE;
     if (!x || !out[0] || !out[1] || (r > 0 && (!xa || !b_stack))) return -CT_EINVAL_POINTER;
     if (ldx < k || ldo[0] < n[0] || ldo[1] < n[1]) return -CT_EINVAL_SHAPE;
     if (k == 0) return -CT_EINVAL_SHAPE;
@@ -2026,9 +2029,7 @@ extern "C" int ct_group_forward(const void *x, int64_t ldx, int32_t count, const
     int tile = choose_tile(m, nt, 1);
     while (tile < TILE_64 && n[0] % kTileEdge[tile]) ++tile;
     pr.tile = tile;
-    // The few-row kernels do not take the column switch, and without a workspace the
-    // split route is not taken: the tiled kernels only.
-    if (m <= 64) return -CT_EINVAL_SHAPE;
+    // Without a workspace the split route is not taken: the tiled kernels only.
     pr.ws = nullptr;
     pr.ws_bytes = 0;
     pr.vec = vec_ok(pr) && aligned16(out[1]) && ldo[1] % 8 == 0;

@@ -218,3 +218,30 @@ def test_group_forward_matches_per_projection_forward(m, k, widths, r, nf4, bias
                                xa[:, i * r:(i + 1) * r], m, n, k, r, biases[i])
         torch.cuda.synchronize()
         assert torch.equal(outs[i].view(torch.int16), want.view(torch.int16)), i
+
+
+def test_group_forward_rejects_invalid_descriptions():
+    """ct_group_forward's checks run on the host, before any launch: the first width must
+    start a tile (a multiple of 64), xa must hold both ranks, exactly one weight per
+    projection, and a few-row call is left to the per-projection path."""
+    lib = _native.library()
+    k, r = 64, 8
+    x = _rand(128, k, seed=1)
+    w = _rand(256, k, seed=2)
+    b_stack = _rand(256, r, seed=3)
+    xa = _rand(128, 2 * r, seed=4)
+    outs = [torch.empty(128, 128, device="cuda", dtype=torch.bfloat16) for _ in range(2)]
+    stream = _native.stream_of(x)
+
+    def call(widths, m=128, ldxa=2 * r, dense=None):
+        n_arr = (ctypes.c_int64 * 2)(*widths)
+        wd = (ctypes.c_void_p * 2)(*(dense if dense is not None else (w.data_ptr(), w.data_ptr())))
+        out_arr = (ctypes.c_void_p * 2)(*[o.data_ptr() for o in outs])
+        ld_arr = (ctypes.c_int64 * 2)(128, 128)
+        return lib.ct_group_forward(x.data_ptr(), k, 2, n_arr, wd, None, b_stack.data_ptr(), xa.data_ptr(), ldxa, None,
+                                    out_arr, ld_arr, m, k, r, None, 0, stream)
+    assert call((96, 128)) == -_shape()                                # 96 columns: not a tile boundary
+    assert call((128, 128), ldxa=r) == -_shape()                       # xa narrower than both ranks
+    assert call((128, 128), dense=(w.data_ptr(), None)) == -_pointer()  # a weight missing
+    assert call((128, 128), m=64) == -_shape()                         # few rows: per projection
+    assert call((128, 128)) == -_workspace()                           # no workspace for [w_1; w_2]
