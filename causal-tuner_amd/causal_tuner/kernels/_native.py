@@ -82,6 +82,9 @@ _SIGNATURES = {
     "ct_group_input_gradient_workspace": (_I64, [_I64, _I32, _P, _P, _I64]),
     "ct_group_input_gradient": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I64,
                                                _I64, _I32, _P, _I64, _P]),
+    "ct_group_input_gradient_lead_workspace": (_I64, [_I64, _I32, _P, _P, _I64]),
+    "ct_group_input_gradient_lead": (ctypes.c_int, [_P, _I64, _P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _I64,
+                                                    _I64, _I64, _I32, _P, _I64, _P]),
     "ct_nf4_quantize_workspace": (_I64, [_I64, _I32, _I32]),
     "ct_nf4_quantize": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "ct_quantize_blockwise": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _P]),
@@ -107,7 +110,7 @@ EXPORTED = tuple(_SIGNATURES)
 _library = None
 
 
-ABI_VERSION = 12   # ct_abi_version() of the library these signatures describe
+ABI_VERSION = 13   # ct_abi_version() of the library these signatures describe
 
 
 def library_path():

@@ -498,6 +498,37 @@ def group_input_gradient(bases, dy, widths, ranks, a_stack, bs, dx, low, add):
     target.finish()
 
 
+def group_input_gradient_lead(bases, dy0, tail, widths, ranks, a_stack, bs, dx, add):
+    """The same dx and low_i for upstream gradients that arrive as separate tensors
+    (linear.py:107-122): dy0 is read in place, tail = [dy_2 | ... | low_1 | low_2 | ...]
+    holds the later upstream gradients side by side and receives the low-rank products
+    after them (ct_group_input_gradient_lead)."""
+    m, k = dx.shape
+    count = len(bases)
+    dy0, lddy0 = _rows(dy0)
+    written, ldtail = _rows(tail)
+    if written.data_ptr() != tail.data_ptr():
+        raise ValueError("group_input_gradient_lead: tail must be a 16-byte aligned matrix with unit row stride")
+    target = _Output(dx)
+    if add and target.buffer is not dx:
+        target.buffer.copy_(dx)
+    descs = [base.desc if base.state is not None else None for base in bases]
+    dense = (ctypes.c_void_p * count)(*[None if d is not None else base.matrix.data_ptr()
+                                        for base, d in zip(bases, descs)])
+    packed = (ctypes.POINTER(_native.NF4Weight) * count)(*[None if d is None else ctypes.pointer(d) for d in descs])
+    factors = (ctypes.c_void_p * count)(*[b.contiguous().data_ptr() for b in bs])
+    n_arr, r_arr = (ctypes.c_int64 * count)(*widths), (ctypes.c_int64 * count)(*ranks)
+    lib = _native.library()
+    ws = _workspace(lib.ct_group_input_gradient_lead_workspace(m, count, n_arr, r_arr, k), dx.device)
+    with _native.device_of(dx):
+        status = lib.ct_group_input_gradient_lead(
+            _native.ptr(dy0), lddy0, _native.ptr(tail), ldtail, count, n_arr, r_arr, dense, packed,
+            _native.ptr(a_stack.contiguous()), factors, _native.ptr(target.buffer), target.ld, m, k, int(add),
+            _native.ptr(ws), ws.numel(), _native.stream_of(dx))
+    _native.check(status, "ct_group_input_gradient_lead")
+    target.finish()
+
+
 # From this many rows ct_forward_linear decodes an NF4 weight before its dense GEMM; two
 # projections that share an input then run their forward as one GEMM (ct_group_forward).
 GROUP_FORWARD_ROWS = 512
@@ -798,22 +829,25 @@ class _LoRAGroup(torch.autograd.Function):
         xa = None if kept else torch.empty((span, sum(ranks)), device=x.device, dtype=ctx.dtype)
         rotated = min(count, 2) if ctx.head_dim else 0
         widths = [signal.shape[1] for signal in signals]
-        # From GROUP_DX_ROWS rows the group's input gradient is one contraction over the
-        # upstream gradients side by side (the q/k ones rotated back into their columns)
-        # and the weights decoded side by side: dx is rounded once instead of after every
-        # projection, and k and v add no pass over dx.
-        # The upstream gradients arrive as separate tensors: the ones not rotated on the way
-        # in are copied side by side, which pays only while the copies move fewer bytes than
-        # the dx passes the one contraction saves (one read and write of dx per projection
-        # after the first): q/k/v, not two wide projections such as gate and up.
-        copied = sum(widths[rotated:])
+        # From GROUP_DX_ROWS rows the group's input gradient is one contraction
+        # (ct_group_input_gradient_lead): the first upstream gradient read in place (or
+        # rotated back into a buffer of its own), the later ones side by side ahead of the
+        # low-rank products in one tail matrix, so dx is rounded once instead of after every
+        # projection and k and v add no pass over dx.
+        # The later upstream gradients arrive as separate tensors: the ones not rotated on
+        # the way in are copied into the tail, which pays only while the copies move fewer
+        # bytes than the dx passes the one contraction saves (one read and write of dx per
+        # projection after the first): q/k/v, not two wide projections such as gate and up.
+        copied = sum(widths[max(rotated, 1):])
         grouped = (dx is not None and x.is_cuda and ctx.dtype == torch.bfloat16
                    and group_dx_ready(bases, widths, ranks, span) and copied < (count - 1) * flat.shape[1])
         if grouped:
-            joined = torch.empty((span, sum(widths)), device=x.device, dtype=ctx.dtype)
-            low = torch.empty((span, sum(ranks)), device=x.device, dtype=ctx.dtype)
+            n_tail = sum(widths[1:])
+            tail = torch.empty((span, n_tail + sum(ranks)), device=x.device, dtype=ctx.dtype)
+            low = tail[:, n_tail:]
+            head = torch.empty((span, widths[0]), device=x.device, dtype=ctx.dtype) if rotated else None
             a_stack = stack if stack is not None else stacked_rows([factors[2*i] for i in range(count)])
-            columns = [slice(sum(widths[:i]), sum(widths[:i+1])) for i in range(count)]
+            columns = [None] + [slice(sum(widths[1:i]), sum(widths[1:i+1])) for i in range(1, count)]
             low_columns = [slice(sum(ranks[:i]), sum(ranks[:i+1])) for i in range(count)]
         else:
             low = torch.empty((span, max(ranks)), device=x.device, dtype=ctx.dtype)
@@ -845,18 +879,20 @@ class _LoRAGroup(torch.autograd.Function):
                 tile_signals = []
                 for index in range(count):
                     signal = signals[index][start:start+n_part]
-                    target = joined[:n_part, columns[index]]
+                    if index == 0:   # read in place unless rotated back into a buffer of its own
+                        target = head[:n_part] if rotated else None
+                    else:
+                        target = tail[:n_part, columns[index]]
                     if index < rotated:
                         from .core_cuda import inverse_rope_tile
                         signal = inverse_rope_tile(signal, cosine[start:start+n_part],
                                                    sine[start:start+n_part], ctx.head_dim, target)
-                    else:
+                    elif index > 0:
                         target.copy_(signal)
                         signal = target
                     tile_signals.append(signal)
-                group_input_gradient(bases, joined[:n_part], widths, ranks, a_stack,
-                                     [factors[2*i+1] for i in range(count)], dx[start:start+n_part],
-                                     low[:n_part], False)
+                group_input_gradient_lead(bases, tile_signals[0], tail[:n_part], widths, ranks, a_stack,
+                                          [factors[2*i+1] for i in range(count)], dx[start:start+n_part], False)
                 for index in range(count if run is None else run[0]):
                     inputs = (kept[index][start:start+n_part] if kept else
                               xa[:n_part, sum(ranks[:index]):sum(ranks[:index+1])])
@@ -864,8 +900,8 @@ class _LoRAGroup(torch.autograd.Function):
                                         low[:n_part, low_columns[index]], inputs, add=start > 0)
                 if run is not None:
                     inputs = kept_run[start:start+n_part] if kept else xa[:n_part, r_lo:r_hi]
-                    parameter_gradients(part, joined[:n_part, n_lo:n_hi], run_da, run_db, low[:n_part, r_lo:r_hi],
-                                        inputs, add=start > 0)
+                    parameter_gradients(part, tail[:n_part, n_lo - widths[0]:n_hi - widths[0]], run_da, run_db,
+                                        low[:n_part, r_lo:r_hi], inputs, add=start > 0)
                 continue
             window = slice(start, start+n_part)
             for index in range(count):

@@ -1699,7 +1699,7 @@ bool nf4_fusable(const ct_nf4_weight *w) {
 
 using namespace ct;
 
-extern "C" int ct_abi_version(void) { return 12; }
+extern "C" int ct_abi_version(void) { return 13; }
 
 extern "C" const char *ct_status_string(int status) {
     switch (status) {
@@ -2235,6 +2235,123 @@ extern "C" int ct_group_input_gradient(const void *dy, int64_t lddy, int32_t cou
     pr.p.seg[1].b = dense(a_stack, k);
     pr.p.seg[1].k = rt;
     pr.p.nseg = rt > 0 ? 2 : 1;
+    pr.p.m = m;
+    pr.p.n = k;
+    pr.p.c = dx;
+    pr.p.ldc = lddx;
+    pr.p.beta = add;
+    pr.src[0] = SRC_KC;
+    pr.src[1] = SRC_KC;
+    pr.src[2] = SRC_KC;
+    pr.src[3] = SRC_KS;
+    pr.out = CT_BF16;
+    pr.splits = 1;
+    pr.tile = -1;
+    pr.ws = workspace;
+    pr.ws_bytes = workspace ? workspace_bytes : 0;
+    pr.vec = vec_ok(pr);
+    const int slot = profile_open(CT_PROF_DX_GEMM, stream);
+    const hipError_t e = run(pr, stream);
+    profile_close(slot, stream, 2.0 * m * k * (double)(nt + rt));
+    return to_status(e);
+}
+
+// The workspace of ct_group_input_gradient_lead: w_0^T [k, n_0], then the tail's B operand
+// [w_1; ...; w_{count-1}; a_stack] [n_tail + r_total, k], then the larger of the low-rank
+// products' and the contraction's split partials.
+extern "C" int64_t ct_group_input_gradient_lead_workspace(int64_t m, int32_t count, const int64_t *n,
+                                                          const int64_t *r, int64_t k) {
+    int64_t nt, rt;
+    if (m <= 0 || k <= 0 || group_widths(count, n, r, &nt, &rt)) return 0;
+    int64_t low = 0;
+    for (int i = 0; i < count; ++i) {
+        const int64_t w = r[i] > 0 ? ct_gemm_workspace(m, r[i], n[i], 0, 0, CT_BF16) : 0;
+        low = w > low ? w : low;
+    }
+    const int64_t ks[2] = {n[0], nt - n[0] + rt};
+    const int sb[2] = {SRC_KC, SRC_KS};
+    const int64_t main = problem_workspace(m, k, ks, ks[1] > 0 ? 2 : 1, sb);
+    return weight_bytes(n[0], k) + weight_bytes(nt - n[0] + rt, k) + (low > main ? low : main);
+}
+
+extern "C" int ct_group_input_gradient_lead(const void *dy0, int64_t lddy0, void *tail, int64_t ldtail,
+                                            int32_t count, const int64_t *n, const int64_t *r,
+                                            const void *const *w_dense, const ct_nf4_weight *const *w_nf4,
+                                            const void *a_stack, const void *const *b, void *dx, int64_t lddx,
+                                            int64_t m, int64_t k, int32_t add, void *workspace,
+                                            int64_t workspace_bytes, hipStream_t stream) {
+    int64_t nt, rt;
+    if (m < 0 || k < 0 || group_widths(count, n, r, &nt, &rt)) return -CT_EINVAL_SHAPE;
+    if (m == 0 || k == 0) return 0;
+    const int64_t n0 = n[0], ntail = nt - n0, kt = ntail + rt;  // the tail's reduction
+    if (!dy0 || !dx || (kt > 0 && !tail) || (rt > 0 && (!a_stack || !b))) return -CT_EINVAL_POINTER;
+    if (lddy0 < n0 || lddx < k || (kt > 0 && ldtail < kt)) return -CT_EINVAL_SHAPE;
+    for (int i = 0; i < count; ++i) {
+        const void *wd = w_dense ? w_dense[i] : nullptr;
+        const ct_nf4_weight *wq = w_nf4 ? w_nf4[i] : nullptr;
+        if (n[i] % 8) return -CT_EINVAL_SHAPE;  // 16-byte aligned column blocks
+        if (!wd == !wq || (r[i] > 0 && !b[i])) return -CT_EINVAL_POINTER;
+        if (wq) {
+            if (const int st = validate_nf4(wq)) return st;
+            if (wq->rows != n[i] || wq->cols != k) return -CT_EINVAL_SHAPE;
+            if (i == 0 && !nf4_transposable(wq)) return -CT_EINVAL_LAYOUT;
+        }
+    }
+    void *w0buf = nullptr, *wtail = nullptr;
+    if (const int st = take_weight(workspace, workspace_bytes, n0, k, w0buf)) return st;
+    if (kt > 0)
+        if (const int st = take_weight(workspace, workspace_bytes, kt, k, wtail)) return st;
+    // w_0^T [k, n_0] for the first projection's reduction-contiguous segment
+    if (w_nf4 && w_nf4[0]) {
+        if (const hipError_t e = nf4_dequant_transposed(w_nf4[0], w0buf, stream, n0); e != hipSuccess)
+            return to_status(e);
+    } else {
+        transpose_bf16<<<dim3((unsigned)cdiv(k, 64), (unsigned)cdiv(n0, 64)), 256, 0, stream>>>(
+            static_cast<const uint16_t *>(w_dense[0]), k, n0, k, static_cast<uint16_t *>(w0buf), n0);
+        if (const hipError_t e = hipGetLastError(); e != hipSuccess) return to_status(e);
+    }
+    // The tail's B operand, rows of its reduction: w_1 .. w_{count-1} in their own layout
+    // (w_i [n_i, k]: row j of w_i multiplies column j of dy_i), then a_stack.
+    int64_t row = 0;
+    for (int i = 1; i < count; ++i) {
+        uint16_t *dst = static_cast<uint16_t *>(wtail) + row * k;
+        if (w_nf4 && w_nf4[i]) {
+            if (const int st = ct_nf4_dequant(w_nf4[i], dst, CT_BF16, stream)) return st;
+        } else {
+            const hipError_t e = hipMemcpyAsync(dst, w_dense[i], (size_t)(n[i] * k * 2), hipMemcpyDeviceToDevice,
+                                                stream);
+            if (e != hipSuccess) return to_status(e);
+        }
+        row += n[i];
+    }
+    if (rt > 0) {
+        const hipError_t e = hipMemcpyAsync(static_cast<uint16_t *>(wtail) + ntail * k, a_stack, (size_t)(rt * k * 2),
+                                            hipMemcpyDeviceToDevice, stream);
+        if (e != hipSuccess) return to_status(e);
+    }
+    // low_i = dy_i b_i into the tail's columns after the upstream gradients
+    int64_t col = 0, rcol = ntail;
+    for (int i = 0; i < count; ++i) {
+        if (r[i] > 0) {
+            const void *a = i == 0 ? dy0 : static_cast<const void *>(static_cast<const uint16_t *>(tail) + col);
+            const int slot = profile_open(CT_PROF_LOWRANK, stream);
+            const int st = ct_gemm(a, i == 0 ? lddy0 : ldtail, 0, b[i], r[i], 0, static_cast<uint16_t *>(tail) + rcol,
+                                   ldtail, CT_BF16, nullptr, 0, m, r[i], n[i], workspace, workspace_bytes, stream);
+            profile_close(slot, stream, 2.0 * m * r[i] * n[i]);
+            if (st) return st;
+        }
+        if (i > 0) col += n[i];
+        rcol += r[i];
+    }
+    // dx (+)= dy_0 w_0^T-segment + tail [w_1; ...; a_stack]: one contraction, rounded once
+    Problem pr{};
+    pr.p.seg[0].a = dense(dy0, lddy0);
+    pr.p.seg[0].b = dense(w0buf, n0);
+    pr.p.seg[0].k = n0;
+    pr.p.seg[1].a = dense(tail, ldtail);
+    pr.p.seg[1].b = dense(wtail, k);
+    pr.p.seg[1].k = kt;
+    pr.p.nseg = kt > 0 ? 2 : 1;
     pr.p.m = m;
     pr.p.n = k;
     pr.p.c = dx;

@@ -421,6 +421,32 @@ int ct_group_input_gradient(const void *dy, int64_t lddy, int32_t count, const i
                             void *workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Replaces the same dx half (kernels/linear.py:107-122) where the upstream gradients
+ * arrive as separate tensors: the first projection's dy_0 is read where it lies, so no
+ * [m, n_total] side-by-side copy is made of it. For i < count (count <= CT_GROUP_MAX):
+ *   low_i = bf16(dy_i b_i)                                    [m, r_i]
+ *   dx    = bf16(dy_0 w_0 + tail [w_1; ...; w_{count-1}; a_stack] (+ dx if add))   [m, k]
+ * where tail [m, n_tail + r_total] (ldtail, n_tail = n_1 + ... + n_{count-1}) holds
+ * dy_1 .. dy_{count-1} side by side in its first n_tail columns on entry and receives
+ * low_0 .. low_{count-1} side by side in the rest. The sum is one contraction over
+ * n_total + r_total reduction columns, fp32-accumulated and rounded once, as in
+ * ct_group_input_gradient (the two differ only in the order of the fp32 additions).
+ * dy_0 [m, n_0] (lddy0); weights, a_stack and b as for ct_group_input_gradient, except
+ * that only w_0 needs the transposed decode: w_0 is decoded (or, dense, transposed) into
+ * [k, n_0] and the others in their own layout [n_i, k], beside a copy of a_stack, in the
+ * workspace (ct_group_input_gradient_lead_workspace); the low-rank products and the
+ * contraction's split partials use the rest. For projections whose later members are
+ * narrow (q with k and v: 256 copied columns instead of 4352).
+ */
+int64_t ct_group_input_gradient_lead_workspace(int64_t m, int32_t count, const int64_t *n, const int64_t *r,
+                                               int64_t k);
+int ct_group_input_gradient_lead(const void *dy0, int64_t lddy0, void *tail, int64_t ldtail, int32_t count,
+                                 const int64_t *n, const int64_t *r, const void *const *w_dense,
+                                 const ct_nf4_weight *const *w_nf4, const void *a_stack, const void *const *b,
+                                 void *dx, int64_t lddx, int64_t m, int64_t k, int32_t add, void *workspace,
+                                 int64_t workspace_bytes, hipStream_t stream);
+
+/*
  * Replaces parameter_gradients (kernels/linear.py:42-44) with accumulate's fp32 branch
  * (kernels/linear.py:16-24):
  *   da = low^T x   (+ da if add)   float32 [r, k]

@@ -43,7 +43,7 @@ def test_library_embeds_gfx950_code_objects():
 
 def test_status_strings_and_version():
     lib = _native.library()
-    assert lib.ct_abi_version() == 12
+    assert lib.ct_abi_version() == 13
     assert lib.ct_status_string(0) == b"success"
     assert b"workspace" in lib.ct_status_string(-5)
     assert b"fused" in lib.ct_status_string(-6)

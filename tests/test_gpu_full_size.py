@@ -14,7 +14,7 @@ rounding points of the reference's sequence (kernels/linear.py:27-44): xa and lo
 bf16, outputs and input gradients rounded to bf16 once per accumulation. Outputs and input
 gradients must be within 1e-3 in relative Frobenius norm of that fp32 result (the bar of
 the north star's fp32-accumulated oracle) and within 2e-2 in max-abs relative error; q/k/v's
-dx, which from 257 rows is one contraction rounded once (ct_group_input_gradient), is held
+dx, which from 257 rows is one contraction rounded once (ct_group_input_gradient_lead), is held
 to 1e-3 of the fp32 sum rounded once and to 2e-2 (max-abs relative) of the reference's
 per-projection rounding; dA/dB
 (fp32 outputs of bf16 products) within 1e-3; a repeated backward bit-identical

@@ -14,7 +14,13 @@ and of the MLP's gate/up, kernels/mlp_cuda.py:136-140):
   previous dx with add) rounded once to bf16, and within 2e-2 (max-abs relative) of the
   reference's sequence of per-projection input gradients, which rounds after each one;
 * a repeated call is bit-identical; NF4 and dense weights; invalid descriptions are
-  refused on the host."""
+  refused on the host.
+
+ct_group_input_gradient_lead: the same dx and low_i with the first upstream gradient read
+in place and the later ones in a tail matrix ahead of the low-rank products it receives:
+low_i bit-identical to ct_input_gradient's, dx within 1e-3 of the same float64 sum, within
+one bf16 rounding step of ct_group_input_gradient's (the fp32 additions run in another
+order), bit-identical on a repeated call, with pitched operands."""
 
 import ctypes
 
@@ -123,6 +129,117 @@ def test_group_input_gradient_against_float64_and_per_projection(m, k, widths, r
     assert (diff.norm() / want.norm()).item() <= 1e-3
     peak = ((dx.float() - sequence).abs().max() / sequence.abs().max()).item()
     assert peak <= 2e-2, peak
+
+
+def _call_lead(m, k, widths, ranks, weights, dy0, tail, a_stack, bs, dx, add, ws_extra=0):
+    lib = _native.library()
+    count = len(widths)
+    n_arr, r_arr = (ctypes.c_int64 * count)(*widths), (ctypes.c_int64 * count)(*ranks)
+    dense = (ctypes.c_void_p * count)(*[w.data_ptr() if isinstance(w, torch.Tensor) else None for w in weights])
+    descs = [None if isinstance(w, torch.Tensor) else _native.nf4_descriptor(*w) for w in weights]
+    packed = (ctypes.POINTER(_native.NF4Weight) * count)(*[None if d is None else ctypes.pointer(d) for d in descs])
+    factors = (ctypes.c_void_p * count)(*[b.data_ptr() for b in bs])
+    need = lib.ct_group_input_gradient_lead_workspace(m, count, n_arr, r_arr, k) + ws_extra
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    return lib.ct_group_input_gradient_lead(dy0.data_ptr(), dy0.stride(0), tail.data_ptr(), tail.stride(0), count,
+                                            n_arr, r_arr, dense, packed, a_stack.data_ptr(), factors, dx.data_ptr(),
+                                            dx.stride(0), m, k, int(add), ws.data_ptr(), need,
+                                            _native.stream_of(dx))
+
+
+@pytest.mark.parametrize("m,k,widths,ranks,nf4", CASES + [(8192, 512, (512, 64, 64), (32, 32, 32), True)])
+@pytest.mark.parametrize("add", [False, True])
+def test_group_input_gradient_lead_against_float64_and_joined(m, k, widths, ranks, nf4, add):
+    print(f"group dx lead: m={m} k={k} widths={widths} ranks={ranks} nf4={nf4} add={add}", flush=True)
+    count = len(widths)
+    weights, dense = [], []
+    for i, n in enumerate(widths):
+        w = _rand(n, k, seed=10 + i, scale=0.02)
+        if nf4:
+            packed, state = quantize_nf4(w)
+            weights.append((packed, state))
+            dense.append(_decode(packed, state))
+        else:
+            weights.append(w)
+            dense.append(w)
+    a_stack = _rand(sum(ranks), k, seed=20, scale=0.05)
+    a_list = list(torch.split(a_stack, list(ranks)))
+    bs = [_rand(n, r, seed=30 + i, scale=0.05) for i, (n, r) in enumerate(zip(widths, ranks))]
+    dy = _rand(m, sum(widths), seed=40)
+    prior = _rand(m, k, seed=41)
+    n0, ntail, rt = widths[0], sum(widths[1:]), sum(ranks)
+    # dy_0 as a column block of a wider matrix, the tail pitched past its n_tail + r_total
+    wide = torch.full((m, n0 + 24), float("nan"), device="cuda", dtype=torch.bfloat16)
+    wide[:, 8:8 + n0] = dy[:, :n0]
+    dy0 = wide[:, 8:8 + n0]
+    store = torch.full((m, ntail + rt + 16), float("nan"), device="cuda", dtype=torch.bfloat16)
+    tail = store[:, :ntail + rt]
+    tail[:, :ntail] = dy[:, n0:]
+    dx = prior.clone() if add else torch.full((m, k), float("nan"), device="cuda", dtype=torch.bfloat16)
+    assert _call_lead(m, k, widths, ranks, weights, dy0, tail, a_stack, bs, dx, add) == 0
+    again_store = store.clone()
+    again_store[:, ntail:ntail + rt] = float("nan")
+    again_dx = prior.clone() if add else torch.empty_like(dx)
+    assert _call_lead(m, k, widths, ranks, weights, dy0, again_store[:, :ntail + rt], a_stack, bs, again_dx,
+                      add) == 0
+    joined_dx = prior.clone() if add else torch.empty_like(dx)
+    joined_low = torch.empty(m, rt, device="cuda", dtype=torch.bfloat16)
+    assert _call(m, k, widths, ranks, weights, dy, a_stack, bs, joined_dx, joined_low, add) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(dx.view(torch.int16), again_dx.view(torch.int16))
+    assert torch.equal(store.view(torch.int16), again_store.view(torch.int16))
+    low = tail[:, ntail:]
+    assert torch.equal(low.view(torch.int16), joined_low.view(torch.int16))   # the same rank-r products
+    assert torch.equal(tail[:, :ntail].view(torch.int16), dy[:, n0:].view(torch.int16))   # read only
+    cols = [sum(widths[:i]) for i in range(count + 1)]
+    rcols = [sum(ranks[:i]) for i in range(count + 1)]
+    want = prior.double() if add else torch.zeros(m, k, device="cuda", dtype=torch.float64)
+    for i in range(count):
+        dyi = dy[:, cols[i]:cols[i + 1]]
+        want += dyi.double() @ dense[i].double() + low[:, rcols[i]:rcols[i + 1]].double() @ a_list[i].double()
+        if m <= 1024:
+            _, single_low = _single(dyi.contiguous(), weights[i], a_list[i].contiguous(), bs[i], m, widths[i], k,
+                                    ranks[i])
+            assert torch.equal(low[:, rcols[i]:rcols[i + 1]].view(torch.int16), single_low.view(torch.int16)), i
+    want = want.to(torch.bfloat16).float()
+    assert bool(torch.isfinite(dx.float()).all())
+    assert ((dx.float() - want).norm() / want.norm()).item() <= 1e-3
+    # both round one fp32 sum once: apart from rounding flips, one step of bf16 (2^-7 relative
+    # to the larger magnitude) at most
+    step = torch.maximum(dx.float().abs(), joined_dx.float().abs()) * 2.0 ** -7 + 1e-6
+    assert bool(((dx.float() - joined_dx.float()).abs() <= step).all())
+
+
+def test_group_input_gradient_lead_refuses_invalid_descriptions():
+    lib = _native.library()
+    m, k = 64, 64
+    w = _rand(16, k, seed=1)
+    dy0 = _rand(m, 16, seed=2)
+    tail = _rand(m, 16 + 8, seed=5)
+    a = _rand(8, k, seed=3)
+    b = _rand(16, 4, seed=4)
+    dx = torch.empty(m, k, device="cuda", dtype=torch.bfloat16)
+    stream = _native.stream_of(dy0)
+
+    def call(widths, ranks, dense, ldtail=24, tail_ptr=True, ws=None, count=None):
+        count = len(widths) if count is None else count
+        n_arr = (ctypes.c_int64 * max(len(widths), 1))(*widths)
+        r_arr = (ctypes.c_int64 * max(len(ranks), 1))(*ranks)
+        wd = (ctypes.c_void_p * max(len(dense), 1))(*dense)
+        bb = (ctypes.c_void_p * max(len(widths), 1))(*[b.data_ptr()] * len(widths))
+        return lib.ct_group_input_gradient_lead(dy0.data_ptr(), 16, tail.data_ptr() if tail_ptr else None, ldtail,
+                                                count, n_arr, r_arr, wd, None, a.data_ptr(), bb, dx.data_ptr(), k,
+                                                m, k, 0, None if ws is None else ws.data_ptr(),
+                                                0 if ws is None else ws.numel(), stream)
+    pair = (w.data_ptr(), w.data_ptr())
+    assert call((16, 12), (4, 4), pair) == -_shape()                        # a width not a multiple of 8
+    assert call((), (), (), count=0) == -_shape()                           # no projections
+    assert call((16, 16), (4, 4), (w.data_ptr(), None)) == -_pointer()      # a weight missing
+    assert call((16, 16), (4, 4), pair, tail_ptr=False) == -_pointer()      # no tail
+    assert call((16, 16), (4, 4), pair, ldtail=23) == -_shape()             # tail narrower than 16 + 8
+    assert call((16, 16), (4, 4), pair) == -_workspace()                    # no workspace for the weights
+    small = torch.empty(4096, dtype=torch.uint8, device="cuda")
+    assert call((16, 16), (4, 4), pair, ws=small) == -_workspace()          # too small for both
 
 
 def test_group_input_gradient_refuses_invalid_descriptions():
