@@ -362,3 +362,61 @@ def test_group_forward_rejects_invalid_descriptions():
     assert call((128, 128), dense=(w.data_ptr(), None)) == -_pointer()  # a weight missing
     assert call((128, 128), m=64) == -_shape()                         # few rows: per projection
     assert call((128, 128)) == -_workspace()                           # no workspace for [w_1; w_2]
+
+
+@pytest.mark.parametrize("nf4", [False, True])
+def test_rotated_group_backward_against_float64(nf4, monkeypatch):
+    """q/k/v through project_group with rotary (q and k rotated, v not) at 300 rows, where the
+    input gradient is one grouped contraction with q's upstream gradient rotated back into a
+    buffer of its own and k's beside v's in the tail: every gradient within 1e-2 (relative
+    Frobenius) of float64 autograd through the reference's host rotation
+    (modeling/rotary.py's formula, kernels/linear.py:59-130's product sequence) with the
+    same bf16 base weights."""
+    from causal_tuner.kernels import linear
+    from causal_tuner.kernels.linear import project_group
+    from causal_tuner.modeling.lora import Projection
+    from causal_tuner.modeling.rotary import rotate
+    print(f"rotated q/k/v group backward vs float64 nf4={nf4}", flush=True)
+    tokens, width, head_dim = 300, 512, 128
+    calls = []
+    original = linear.group_input_gradient_lead
+
+    def counted(*args, **kwargs):
+        calls.append(1)
+        return original(*args, **kwargs)
+    monkeypatch.setattr(linear, "group_input_gradient_lead", counted)
+    modules = []
+    for i, n in enumerate((1024, 256, 256)):
+        torch.manual_seed(50 + i)
+        module = Projection(width, n, bias=True, rank=16, device="cuda")
+        if nf4:
+            module.install_nf4(module.weight.detach().clone(), "cuda")
+        torch.nn.init.normal_(module.lora_B, std=0.05)
+        torch.nn.init.normal_(module.bias, std=0.1)
+        modules.append(module)
+    x = _rand(tokens, width, seed=60)
+    angle = torch.rand(tokens, 32, device="cuda", generator=torch.Generator(device="cuda").manual_seed(61)) * 1e3
+    cosine, sine = angle.cos().bfloat16(), angle.sin().bfloat16()
+    xd = x.clone().requires_grad_(True)
+    outs = project_group(modules, xd, rotary=(cosine, sine, head_dim))
+    signals = [_rand(*t.shape, seed=70 + i) for i, t in enumerate(outs)]
+    params = [xd, *(p for m in modules for p in (m.lora_A, m.lora_B))]
+    grads = torch.autograd.grad(outs, params, signals)
+    assert calls, "the grouped contraction did not run"
+
+    x64 = x.double().cpu().requires_grad_(True)
+    factors = [(m.lora_A.detach().double().cpu().requires_grad_(True),
+                m.lora_B.detach().double().cpu().requires_grad_(True)) for m in modules]
+    c64, s64 = cosine.double().cpu(), sine.double().cpu()
+    outs64 = []
+    for i, (m, (a, b)) in enumerate(zip(modules, factors)):
+        w = m.base_weight().detach().double().cpu()
+        y = x64 @ w.T + (x64 @ a.T) @ b.T + m.bias.detach().double().cpu()
+        if i < 2:
+            y = rotate(y.reshape(tokens, -1, head_dim), c64, s64).reshape(tokens, -1)
+        outs64.append(y)
+    want = torch.autograd.grad(outs64, [x64, *(t for pair in factors for t in pair)],
+                               [s.double().cpu() for s in signals])
+    for index, (got, ref) in enumerate(zip(grads, want)):
+        err = ((got.double().cpu() - ref).norm() / ref.norm()).item()
+        assert err <= 1e-2, (index, err)
