@@ -923,7 +923,8 @@ class _LoRAGroup(torch.autograd.Function):
             for index in range(*run):
                 cols = slice(sum(widths[:index]) - n_lo, sum(widths[:index+1]) - n_lo)
                 rows = slice(sum(ranks[:index]) - r_lo, sum(ranks[:index+1]) - r_lo)
-                gradients[index][0].copy_(run_da[rows])
+                # dA: consecutive rows of the run's output, handed out as contiguous views
+                gradients[index] = (run_da[rows], gradients[index][1])
                 gradients[index][1].copy_(run_db[cols, rows])
         del bases, factors, stack
         results = [value for da, db in gradients for value in (None, da, db, None)]
